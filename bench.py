@@ -1,0 +1,312 @@
+#!/usr/bin/env python3
+"""Benchmark: SiHC fused read+write, forward + backward, at the SiHC-XL shape.
+
+Workload: batch 256, 16x16 workspace tokens (256 per image), 4
+slots per token (32x32 carrier), D = 1152, 28 layers x 2 sublayers = 56 connection
+events, bf16 storage with fp32 accumulation. One step is the whole read/write path of
+one batch: every event's fused write+read forward and its fused backward (carrier,
+workspace-update and weight gradients), run as the literal per-event schedule
+
+    z_0 = read(X_0);  X_{i+1}, z_{i+1} = write+read(X_i, dz_i);  ...  X_56 = write(X_55)
+
+with each carrier element crossing HBM once per event. The sublayer bodies are not
+part of the path: their outputs dz_i ~ N(0,1) and their input gradients
+g_i ~ N(0,1e-2) (and the final carrier gradient ~ N(0,1e-2)) are drawn once before
+timing, all inputs resident in HBM. Kernels are launched straight through the C ABI
+(libsihc_hip.so) on torch's current HIP stream with preallocated outputs.
+
+Prints one JSON line (see the driver contract). `value` is algorithmic HBM GB/s of
+the whole step; tokens/s and the fraction of the 8 TB/s peak ride along.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "residual-stream-burden_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "fused read+write fwd+bwd achieved HBM GB/s (% of peak) + tokens/s at SiHC-XL"
+HBM_PEAK_GBS = 8000.0
+ELEM = 2  # bf16
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--batch", type=int, default=256)
+    p.add_argument("--channels", type=int, default=1152)
+    p.add_argument("--events", type=int, default=56)
+    p.add_argument("--seed", type=int, default=2)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    return p.parse_args()
+
+
+class LiteralStep:
+    """Preallocated buffers and the C-ABI call list of one fwd+bwd step."""
+
+    def __init__(self, batch: int, channels: int, events: int, seed: int):
+        import torch
+
+        from sihc_hip import _lib
+
+        self.torch = torch
+        self.L = _lib.lib()
+        self.check = _lib.check
+        dev = torch.device("cuda", 0)
+        bf = torch.bfloat16
+        g = torch.Generator(device=dev).manual_seed(seed)
+        B, C, E, S, G, K = batch, channels, events, 4, 16, 2
+        self.B, self.C, self.E, self.S, self.G, self.K = B, C, E, S, G, K
+        self.M = B * G * G
+        carrier = (B, G * K, G * K, C)
+        ws = (B, G * G, C)
+
+        def randn(shape, mean=0.0, std=1.0):
+            return (mean + std * torch.randn(shape, device=dev, generator=g)).to(bf)
+
+        # Draw order: X, alpha, beta, dz, upstream grads (BASELINE config 0/2).
+        self.x = [randn(carrier)] + [torch.empty(carrier, device=dev, dtype=bf) for _ in range(E)]
+        self.alpha = torch.stack([randn((S, C), 0.25, 0.02).T.contiguous() for _ in range(E)])  # [E,C,S]
+        self.beta = torch.stack([randn((S, C), 1.0, 0.02).T.contiguous() for _ in range(E)])
+        self.dz = [randn(ws) for _ in range(E)]
+        self.gz = [randn(ws, 0.0, 1e-2) for _ in range(E)]
+        self.h_out = randn(carrier, 0.0, 1e-2)
+        self.z = [torch.empty(ws, device=dev, dtype=bf) for _ in range(E)]
+        self.gx = [torch.empty(carrier, device=dev, dtype=bf) for _ in range(2)]
+        self.gdz = [torch.empty(ws, device=dev, dtype=bf) for _ in range(E)]
+        self.galpha = torch.empty_like(self.alpha)
+        self.gbeta = torch.empty_like(self.beta)
+        nws = self.L.sihc_event_backward_workspace_size(B, G, K, C)
+        self.work = torch.empty((nws + 15) // 16 * 4, device=dev, dtype=torch.float32)
+        self.stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        self._build(E)
+
+    def _build(self, E):
+        L, B, G, K, C = self.L, self.B, self.G, self.K, self.C
+        vp = ctypes.c_void_p
+        p = lambda t: vp(t.data_ptr())  # noqa: E731
+        bf16 = 1
+        work, nwork = p(self.work), self.work.numel() * 4
+        U = self.M * C * ELEM
+        S = self.S
+        w_bytes = C * S * ELEM
+        fwd, bwd = [], []
+        # forward
+        outs = (vp * 1)(self.z[0].data_ptr())
+        fwd.append(("read", L.sihc_read, (p(self.x[0]), p(self.alpha[0]), outs, 1, B, G, K, C, None, bf16,
+                                           self.stream), (S + 1) * U + w_bytes))
+        for i in range(E):
+            last = i == E - 1
+            fwd.append(("event_forward", L.sihc_event_forward,
+                        (p(self.x[i]), p(self.dz[i]), p(self.beta[i]), None if last else p(self.alpha[i + 1]),
+                         p(self.x[i + 1]), None if last else p(self.z[i + 1]), B, G, K, C, None, bf16, self.stream),
+                        ((2 * S + 1) if last else (2 * S + 2)) * U + (1 if last else 2) * w_bytes))
+        # backward: last event (write only, carrier gradient aliased), then full events
+        h = self.h_out
+        bwd.append(("event_backward_last", L.sihc_event_backward,
+                    (p(h), None, None, p(self.dz[E - 1]), p(self.beta[E - 1]), None, None, p(self.gdz[E - 1]),
+                     p(self.gbeta[E - 1]), None, B, G, K, C, None, bf16, bf16, work, nwork, self.stream),
+                    (S + 2) * U + 2 * w_bytes))
+        for i in range(E - 2, -1, -1):
+            dst = self.gx[i % 2]
+            bwd.append(("event_backward", L.sihc_event_backward,
+                        (p(h), p(self.gz[i + 1]), p(self.x[i + 1]), p(self.dz[i]), p(self.beta[i]),
+                         p(self.alpha[i + 1]), p(dst), p(self.gdz[i]), p(self.gbeta[i]), p(self.galpha[i + 1]),
+                         B, G, K, C, None, bf16, bf16, work, nwork, self.stream),
+                        (3 * S + 3) * U + 4 * w_bytes))
+            h = dst
+        # adjoint of the first read (no write part): dX_0 = h + alpha_0 (x) g_0, dalpha_0
+        dst = self.gx[1] if h is self.gx[0] else self.gx[0]
+        bwd.append(("event_backward_first", L.sihc_event_backward,
+                    (p(h), p(self.gz[0]), p(self.x[0]), None, None, p(self.alpha[0]), p(dst), None, None,
+                     p(self.galpha[0]), B, G, K, C, None, bf16, bf16, work, nwork, self.stream),
+                    (3 * S + 1) * U + 2 * w_bytes))
+        self.fwd, self.bwd = fwd, bwd
+        self.bytes_fwd = sum(c[3] for c in fwd)
+        self.bytes_bwd = sum(c[3] for c in bwd)
+
+    def run(self, calls, timer=None):
+        for name, fn, args, _ in calls:
+            if timer is not None and name == "event_backward":
+                start = self.torch.cuda.Event(enable_timing=True)
+                end = self.torch.cuda.Event(enable_timing=True)
+                start.record()
+                self.check(fn(*args))
+                end.record()
+                timer.append((start, end))
+            else:
+                self.check(fn(*args))
+
+    def step(self, timer=None):
+        self.run(self.fwd)
+        self.run(self.bwd, timer)
+
+
+def cpu_baseline(budget_s: float) -> dict:
+    """BASELINE config 0 on the host: the oracle's unfused PyTorch read/write (fp32,
+    batch 8, 256 tokens, 4 slots, D=768, one event) forward + autograd backward."""
+    import torch
+
+    from oracle import sihc_oracle as O
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    torch.manual_seed(0)
+    x = torch.randn(8, 32, 32, 768)
+    alpha = (0.25 + 0.02 * torch.randn(4, 768)).T.contiguous()
+    beta = (1.0 + 0.02 * torch.randn(4, 768)).T.contiguous()
+    y = torch.randn(8, 256, 768)
+    gxp = 1e-2 * torch.randn(8, 32, 32, 768)
+    gz = 1e-2 * torch.randn(8, 256, 768)
+    leaves = [t.clone().requires_grad_() for t in (x, alpha, beta, y)]
+
+    def once():
+        t0 = time.perf_counter()
+        z = O.read_torch(leaves[0], leaves[1])
+        xp = O.write_torch(leaves[0], [leaves[3]], [leaves[2]])
+        t1 = time.perf_counter()
+        torch.autograd.grad((xp * gxp).sum() + (z * gz).sum(), leaves)
+        t2 = time.perf_counter()
+        return t1 - t0, t2 - t1
+
+    for _ in range(3):
+        once()
+    fwd, bwd = [], []
+    t_start = time.perf_counter()
+    while len(fwd) < 20 and (time.perf_counter() - t_start < budget_s or len(fwd) < 3):
+        f, b = once()
+        fwd.append(f)
+        bwd.append(b)
+    U = 8 * 256 * 768 * 4
+    byt = 14 * U + 20 * U  # unfused single event: forward 14 U, backward 20 U (fp32)
+    t = statistics.median(fwd) + statistics.median(bwd)
+    return {
+        "value": round(byt / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "tokens_per_s": round(8 * 256 / t, 1),
+        "fwd_ms": round(statistics.median(fwd) * 1e3, 3), "bwd_ms": round(statistics.median(bwd) * 1e3, 3),
+        "runs": len(fwd),
+        "sample": ("BASELINE config 0 on the host: oracle/ restatement of the reference's unfused PyTorch "
+                   "read_torch/write_torch + autograd, fp32, batch 8 x 256 tokens, 4 slots, D=768, one event "
+                   "fwd+bwd, median of up to 20 runs after 3 warmups; GB/s from the same algorithmic bytes "
+                   "(14 U fwd + 20 U bwd, U = one fp32 workspace tensor)"),
+    }
+
+
+def traffic_from_profiles() -> float | None:
+    """HBM bytes per dominant-kernel launch measured by rocprofv3 counters, if committed."""
+    f = ROOT / "profiles" / "event_backward_traffic.json"
+    if not f.exists():
+        return None
+    try:
+        return float(json.loads(f.read_text())["bytes_per_launch"])
+    except Exception:
+        return None
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build runs no "
+              "multi-GPU path: the read/write path shards along batch with no collective.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (MI355X); none is visible", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+    print(f"[bench] building step: batch={args.batch} C={args.channels} events={args.events}", file=sys.stderr,
+          flush=True)
+    step = LiteralStep(args.batch, args.channels, args.events, args.seed)
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        step.step()
+    torch.cuda.synchronize()
+    print(f"[bench] warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
+
+    timer: list = []
+    t_fwd: list = []
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        a, b, c = ev(), ev(), ev()
+        a.record()
+        step.run(step.fwd)
+        b.record()
+        step.run(step.bwd, timer)
+        c.record()
+        t_fwd.append((a, b, c))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = wall / args.steps * 1e3
+    fwd_ms = statistics.median(a.elapsed_time(b) for a, b, _ in t_fwd)
+    bwd_ms = statistics.median(b.elapsed_time(c) for _, b, c in t_fwd)
+    kern_ms = [s.elapsed_time(e) for s, e in timer]
+    avg_kernel_ms = sum(kern_ms) / len(kern_ms)
+    print(f"[bench] timed {args.steps} steps: {ms_step:.3f} ms/step", file=sys.stderr, flush=True)
+
+    total_bytes = step.bytes_fwd + step.bytes_bwd
+    gbs = total_bytes / (ms_step * 1e-3) / 1e9
+    dom_bytes = next(c[3] for c in step.bwd if c[0] == "event_backward")
+    achieved = dom_bytes / (avg_kernel_ms * 1e-3) / 1e9
+    traffic = traffic_from_profiles()
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "BASELINE config 2: SiHC-XL-shape fused read/write fwd+bwd, literal per-event schedule",
+            "batch": args.batch, "tokens": 256, "slots": 4, "channels": args.channels,
+            "events": args.events, "schedule": "per-event fused (write+read, one carrier pass per event)",
+            "parallelism": "single GPU",
+        },
+        "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "tokens_per_s": round(args.batch * 256 / (ms_step * 1e-3), 1),
+        "fwd_ms": round(fwd_ms, 3),
+        "bwd_ms": round(bwd_ms, 3),
+        "algorithmic_bytes_per_step": total_bytes,
+        "roofline": {
+            "kernel": "k_event_bwd (sihc_event_backward, full event) incl. its partial-sum finalize",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "bytes_per_launch": dom_bytes,
+            "avg_launch_ms": round(avg_kernel_ms, 4),
+            "launches": len(kern_ms),
+        },
+    }
+    if not args.no_cpu_baseline:
+        print("[bench] CPU baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

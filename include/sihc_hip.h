@@ -1,0 +1,153 @@
+/*
+ * sihc_hip.h -- C ABI of the MI355X (gfx950) SiHC hyper-connection read/write path.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream handle
+ * (passed as void *; NULL means the default stream). Nothing allocates, nothing
+ * synchronises the host: work is enqueued on `stream` and the call returns. Return
+ * value is SIHC_OK or an error code; sihc_last_error() returns the message of the
+ * last failure on the calling thread. Argument errors are detected before any launch.
+ *
+ * Layouts (all packed, row-major; see the reference citations per entry point):
+ *   carrier   x       [batch, grid*cell, grid*cell, channels]   NHWC, "high" grid
+ *   workspace z       [batch, grid*grid, channels]             one row per token
+ *   weights   w       [events, channels, slots]                slots = cell*cell
+ *   token m = b*grid*grid + wy*grid + wx owns the cell of carrier pixels
+ *   (b, wy*cell+uy, wx*cell+ux); its slot index is s = uy*cell + ux.
+ *   index             [batch, grid*grid] int32 or NULL. When given, token (b, n)
+ *                     reads and writes the cell index[b, n] of batch b instead of
+ *                     cell n (the spatially indexed variant). Write-type entry
+ *                     points require each batch row of index to be a permutation.
+ *
+ * dtype codes: SIHC_DTYPE_F32 (IEEE fp32) and SIHC_DTYPE_BF16 (bfloat16). All
+ * arithmetic accumulates in fp32 and rounds once (round-to-nearest-even) per stored
+ * element. Pointer arrays (`updates`, `out`) are host arrays of `events` device
+ * pointers; at most SIHC_MAX_EVENTS.
+ *
+ * Reference: tongtongliang/residual-stream-burden, sihc/models/sihc/sublayer_kernels.py
+ * (Triton kernels launched from torch.library custom ops). Each entry point below
+ * names the launch site it replaces.
+ */
+#ifndef SIHC_HIP_H
+#define SIHC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SIHC_MAX_EVENTS 32
+#define SIHC_ABI_VERSION 1
+
+enum { SIHC_DTYPE_F32 = 0, SIHC_DTYPE_BF16 = 1 };
+enum { SIHC_OK = 0, SIHC_ERR_INVALID = 1, SIHC_ERR_HIP = 2 };
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *sihc_last_error(void);
+/* SIHC_ABI_VERSION of the loaded library. */
+int sihc_abi_version(void);
+
+/* E base reads z_e[m,c] = sum_s alpha[e,c,s] * x[m,s,c], one output tensor per event.
+ * alpha is the stacked [events, channels, slots] weight (no host-side transpose).
+ * Replaces: sublayer_kernels.py:219-232 (`sublayer_read`, launch of `_read` at :230-231,
+ * with the alpha transpose at :224 folded into the kernel's LDS staging). */
+int sihc_read(const void *x, const void *alpha, void *const *out, int events,
+              int64_t batch, int grid, int cell, int channels, const int32_t *index,
+              int dtype, void *stream);
+
+/* out[m,s,c] = (add_x ? x[m,s,c] : 0) + sum_e beta[e,c,s] * updates_e[m,c].
+ * x may be NULL when add_x == 0. x/out use x_dtype; updates/beta use w_dtype
+ * (x_dtype may be fp32 with bf16 updates and weights).
+ * Replaces: sublayer_kernels.py:246-258 (`_write_impl`, launch of `_write` at :255-257). */
+int sihc_write(const void *x, const void *const *updates, const void *beta, void *out,
+               int events, int64_t batch, int grid, int cell, int channels, int add_x,
+               const int32_t *index, int x_dtype, int w_dtype, void *stream);
+
+/* Bytes of device workspace sihc_weight_grad needs for these sizes. */
+size_t sihc_weight_grad_workspace_size(int events, int64_t batch, int grid, int cell,
+                                       int channels);
+/* out[e,c,s] = sum_m x[m,s,c] * z_e[m,c], reduced in fp32 without atomics (per-block
+ * partials in `workspace`, then a fixed-order sum), stored in out_dtype.
+ * Deterministic: identical inputs give identical bits.
+ * Replaces: sublayer_kernels.py:261-273 (`_weights_backward`: zero-init at :264, launch
+ * of `_weight_grad` at :271-272, transpose and cast at :273). */
+int sihc_weight_grad(const void *x, const void *const *z, void *out, int events,
+                     int64_t batch, int grid, int cell, int channels, const int32_t *index,
+                     int dtype, int out_dtype, void *workspace, size_t workspace_bytes,
+                     void *stream);
+
+/* out[m,c] = base[m,c] + sum_j gamma[j,c] * updates_j[m,c] over `active` updates
+ * (1..SIHC_MAX_EVENTS). gamma is [active, channels] in gamma_dtype (fp32 or dtype).
+ * Replaces: sublayer_kernels.py:337-352 (`sublayer_triangular`, launch of `_triangular`
+ * at :350-351). */
+int sihc_triangular(const void *base, const void *const *updates, const void *gamma,
+                    void *out, int active, int64_t rows, int channels, int dtype,
+                    int gamma_dtype, void *stream);
+
+size_t sihc_triangular_gamma_grad_workspace_size(int active, int64_t rows, int channels);
+/* out[j,c] = sum_m grad[m,c] * updates_j[m,c], atomics-free, stored in out_dtype.
+ * Replaces: sublayer_kernels.py:355-361 (`_tri_gamma_backward`, zero-init at :358,
+ * launch of `_triangular_gamma_grad` at :359-360, cast at :361). */
+int sihc_triangular_gamma_grad(const void *grad, const void *const *updates, void *out,
+                               int active, int64_t rows, int channels, int dtype,
+                               int out_dtype, void *workspace, size_t workspace_bytes,
+                               void *stream);
+
+/* One connection event of the literal per-event recurrence, fused into one pass:
+ *   x_out[m,s,c] = x[m,s,c] + beta[c,s] * dz[m,c]                 (write + residual add)
+ *   z_out[m,c]   = sum_s alpha_next[c,s] * x_out[m,s,c]            (next event's read,
+ *                                                                    from the rounded x_out)
+ * beta and alpha_next are single-event [channels, slots] weights. alpha_next/z_out may
+ * be NULL (last event: write only).
+ * No single reference op: fuses `write_torch` then `read_torch` of the literal schedule,
+ * sihc/bench/fusion_controls.py:64 and :80 (`torch_stage`, implementation="literal"). */
+int sihc_event_forward(const void *x, const void *dz, const void *beta,
+                       const void *alpha_next, void *x_out, void *z_out, int64_t batch,
+                       int grid, int cell, int channels, const int32_t *index, int dtype,
+                       void *stream);
+
+size_t sihc_event_backward_workspace_size(int64_t batch, int grid, int cell, int channels);
+/* Adjoint of sihc_event_forward, one pass plus a fixed-order reduction:
+ *   t[m,s,c]       = grad_x_out[m,s,c] + alpha_next[c,s] * grad_z_out[m,c]
+ *   grad_x         = t                                  (stored in dtype)
+ *   grad_dz[m,c]   = sum_s beta[c,s] * t[m,s,c]
+ *   grad_beta[c,s] = sum_m dz[m,c] * t[m,s,c]
+ *   grad_alpha_next[c,s] = sum_m x_out[m,s,c] * grad_z_out[m,c]
+ * Optional parts, so one kernel covers every event of a per-event chain:
+ *   - grad_x_out / grad_z_out may be NULL (zero gradient);
+ *   - read part absent (grad_z_out NULL): alpha_next/x_out unused, grad_alpha_next (if
+ *     given) is zeroed, and grad_x may be NULL, meaning t == grad_x_out is not copied
+ *     (the caller aliases it, as the reference's write backward does);
+ *   - write part absent (beta, dz, grad_dz, grad_beta all NULL): the adjoint of a plain
+ *     read, grad_x = grad_x_out + alpha (x) grad_z_out, grad_alpha = sum x * grad_z_out.
+ * Weight gradients are stored in w_dtype.
+ * Follows the adjoint formulas of sihc/docs/kernel_fusion/README.md:73-84 applied to one
+ * event (the reference's autograd rules sublayer_kernels.py:280-306 with E = 1). */
+int sihc_event_backward(const void *grad_x_out, const void *grad_z_out, const void *x_out,
+                        const void *dz, const void *beta, const void *alpha_next,
+                        void *grad_x, void *grad_dz, void *grad_beta, void *grad_alpha_next,
+                        int64_t batch, int grid, int cell, int channels,
+                        const int32_t *index, int dtype, int w_dtype, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
+/* cells[b,n,s,c] = x[carrier pixel of slot s of cell index[b,n], c]: bit-exact copy of
+ * each token's prediction state into a packed [batch, grid*grid, slots, channels] tile.
+ * No reference counterpart (the spatially indexed variant is defined by this library);
+ * with index == NULL it is the reference's `_high_to_cells`, reference.py:22-35. */
+int sihc_gather_cells(const void *x, const int32_t *index, void *cells, int64_t batch,
+                      int grid, int cell, int channels, int dtype, void *stream);
+/* Inverse of sihc_gather_cells for a permutation index: x[pixel of (index[b,n], s)] =
+ * cells[b,n,s]. With index == NULL it is `_cells_to_high`, reference.py:37-51. */
+int sihc_scatter_cells(const void *cells, const int32_t *index, void *x, int64_t batch,
+                       int grid, int cell, int channels, int dtype, void *stream);
+
+/* Plain device copy of `bytes` bytes (16-byte vectors). No reference counterpart: it is
+ * the calibration kernel for HBM counters and the practical bandwidth ceiling. */
+int sihc_copy(const void *src, void *dst, size_t bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SIHC_HIP_H */

@@ -1,0 +1,1190 @@
+// SiHC hyper-connection read/write path for MI355X (gfx950, CDNA4, wave64).
+//
+// All kernels here are HBM-bound weighted stream reductions and broadcasts over a
+// packed NHWC carrier and packed [tokens, channels] workspace tensors. There is no
+// matrix-core work: per element the path does at most 2*E*S flops per 2*(S+E) bytes.
+//
+// Thread mapping shared by every kernel: a block is (BCG channel groups) x (TL token
+// lanes). A lane owns V adjacent channels (one 16-byte vector for bf16 V=8 / fp32 V=4)
+// and walks a run of tokens with stride TL, so each wave issues fully coalesced
+// 16-byte loads and the per-channel weights of its channel group are fetched once per
+// block: into LDS when the kernel handles many events (read / write / triangular), into
+// registers when it handles one (per-event fused kernels). All sums are fp32 with a
+// single round-to-nearest-even per stored element. Reductions over tokens (weight
+// gradients) are per-thread fp32 partials, then one LDS pass per block that writes a
+// per-block partial row, then a fixed-order sum over blocks: no atomics, deterministic.
+//
+// Reference (behaviour, not code): tongtongliang/residual-stream-burden,
+// sihc/models/sihc/sublayer_kernels.py (Triton `_read`, `_write`, `_weight_grad`,
+// `_triangular`, `_triangular_gamma_grad`) and sihc/bench/fusion_controls.py:14-85.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <type_traits>
+
+#include "sihc_hip.h"
+
+namespace {
+
+using bf16_t = uint16_t;  // bfloat16 storage (upper 16 bits of an IEEE fp32)
+
+template <int N>
+using IC = std::integral_constant<int, N>;
+
+// ----------------------------------------------------------------------------------
+// element conversion
+// ----------------------------------------------------------------------------------
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16_t v) { return __uint_as_float(uint32_t(v) << 16); }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v);
+template <>
+__device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {
+  // Round to nearest, ties to even; every NaN becomes the canonical quiet NaN 0x7fc0
+  // (the same bits torch's float->bfloat16 conversion produces).
+  uint32_t u = __float_as_uint(v);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return bf16_t(0x7fc0);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return bf16_t(u >> 16);
+}
+// Value of v after a round trip through T (what a stored-then-reloaded element holds).
+template <typename T>
+__device__ __forceinline__ float round_as(float v) { return to_f32(from_f32<T>(v)); }
+
+// ----------------------------------------------------------------------------------
+// vector load/store of V elements of T as fp32
+// ----------------------------------------------------------------------------------
+template <int BYTES> struct RawT;
+template <> struct RawT<16> { using type = uint4; };
+template <> struct RawT<8> { using type = uint2; };
+template <> struct RawT<4> { using type = uint32_t; };
+template <> struct RawT<2> { using type = uint16_t; };
+
+template <typename T, int V>
+__device__ __forceinline__ void load_vec(const T* __restrict__ p, float* o) {
+  constexpr int BYTES = V * int(sizeof(T));
+  constexpr int CH = BYTES >= 16 ? 16 : BYTES;
+  constexpr int EPC = CH / int(sizeof(T));
+  using R = typename RawT<CH>::type;
+#pragma unroll
+  for (int q = 0; q < BYTES / CH; ++q) {
+    R r = reinterpret_cast<const R*>(p)[q];
+    T e[EPC];
+    __builtin_memcpy(e, &r, CH);
+#pragma unroll
+    for (int i = 0; i < EPC; ++i) o[q * EPC + i] = to_f32(e[i]);
+  }
+}
+
+template <typename T, int V>
+__device__ __forceinline__ void store_vec(T* __restrict__ p, const float* v) {
+  constexpr int BYTES = V * int(sizeof(T));
+  constexpr int CH = BYTES >= 16 ? 16 : BYTES;
+  constexpr int EPC = CH / int(sizeof(T));
+  using R = typename RawT<CH>::type;
+#pragma unroll
+  for (int q = 0; q < BYTES / CH; ++q) {
+    T e[EPC];
+#pragma unroll
+    for (int i = 0; i < EPC; ++i) e[i] = from_f32<T>(v[q * EPC + i]);
+    R r;
+    __builtin_memcpy(&r, e, CH);
+    reinterpret_cast<R*>(p)[q] = r;
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// geometry
+// ----------------------------------------------------------------------------------
+struct Geo {
+  int M;    // tokens = batch * grid * grid
+  int GG;   // grid * grid
+  int G;    // workspace grid
+  int K;    // cell edge (slots = K*K)
+  int GK;   // carrier edge = G*K
+  int C;    // channels
+};
+
+struct PtrPack {
+  const void* p[SIHC_MAX_EVENTS];
+};
+
+// Carrier pixel of slot 0 of the cell token m reads/writes. Token m = b*GG + n owns
+// cell n of batch b, or cell index[m] in the spatially indexed variant.
+__device__ __forceinline__ int64_t cell_pixel0(int m, const Geo& g, const int32_t* __restrict__ index) {
+  const uint32_t b = uint32_t(m) / uint32_t(g.GG);
+  uint32_t n = uint32_t(m) - b * uint32_t(g.GG);
+  // Out-of-range indices (rejected by the host wrappers) are clamped so that no access
+  // can leave the carrier.
+  if (index) n = min(uint32_t(index[m]), uint32_t(g.GG) - 1u);
+  const uint32_t wy = n / uint32_t(g.G);
+  const uint32_t wx = n - wy * uint32_t(g.G);
+  return (int64_t(b) * g.GK + int64_t(wy) * g.K) * g.GK + int64_t(wx) * g.K;
+}
+
+// Element offset of (pixel0 + slot s) at channel c, s = uy*K + ux.
+template <int K>
+__device__ __forceinline__ int64_t slot_offset(int64_t pix0, int s, const Geo& g, int c) {
+  return (pix0 + int64_t(s / K) * g.GK + (s % K)) * g.C + c;
+}
+
+// ----------------------------------------------------------------------------------
+// read: out_e[m,c] = sum_s alpha[e,c,s] * x[m,s,c]
+// grid (slices, token chunks), block (BCG, TL); LDS holds alpha as [E][S][BC] fp32.
+// ----------------------------------------------------------------------------------
+template <typename T, int V, int K>
+__global__ void __launch_bounds__(256) k_read(const T* __restrict__ x, const T* __restrict__ alpha,
+                                              PtrPack out, const int32_t* __restrict__ index,
+                                              int E, Geo g, int tpb, int nslices) {
+  constexpr int S = K * K;
+  extern __shared__ float lds[];
+  const int BCG = blockDim.x, TL = blockDim.y;
+  const int BC = BCG * V;
+  const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
+  const int cs = slice * BC;
+  const int tid = threadIdx.y * BCG + threadIdx.x;
+  const int nthr = BCG * TL;
+  for (int i = tid; i < E * BC * S; i += nthr) {  // global [e][c][s] -> LDS [e][s][c]
+    const int e = i / (BC * S);
+    const int r = i - e * BC * S;
+    const int cl = r / S;
+    const int s = r - cl * S;
+    const int c = cs + cl;
+    lds[(e * S + s) * BC + cl] = c < g.C ? to_f32(alpha[(int64_t(e) * g.C + c) * S + s]) : 0.f;
+  }
+  __syncthreads();
+  const int cl0 = threadIdx.x * V;
+  const int c0 = cs + cl0;
+  if (c0 >= g.C) return;
+  const int m_begin = chunk * tpb;
+  const int m_end = min(m_begin + tpb, g.M);
+  for (int m = m_begin + threadIdx.y; m < m_end; m += TL) {
+    const int64_t p0 = cell_pixel0(m, g, index);
+    float xv[S][V];
+#pragma unroll
+    for (int s = 0; s < S; ++s) load_vec<T, V>(x + slot_offset<K>(p0, s, g, c0), xv[s]);
+    const int64_t zoff = int64_t(m) * g.C + c0;
+    for (int e = 0; e < E; ++e) {
+      const float* a = lds + e * S * BC + cl0;
+      float acc[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) acc[v] = 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc[v] = fmaf(a[s * BC + v], xv[s][v], acc[v]);
+      store_vec<T, V>(static_cast<T*>(const_cast<void*>(out.p[e])) + zoff, acc);
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// write: out[m,s,c] = (add_x ? x : 0) + sum_e beta[e,c,s] * upd_e[m,c]
+// ----------------------------------------------------------------------------------
+template <typename TX, typename TW, int V, int K>
+__global__ void __launch_bounds__(256) k_write(const TX* __restrict__ x, PtrPack upd,
+                                               const TW* __restrict__ beta, TX* __restrict__ out,
+                                               const int32_t* __restrict__ index, int E, int add_x,
+                                               Geo g, int tpb, int nslices) {
+  constexpr int S = K * K;
+  extern __shared__ float lds[];
+  const int BCG = blockDim.x, TL = blockDim.y;
+  const int BC = BCG * V;
+  const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
+  const int cs = slice * BC;
+  const int tid = threadIdx.y * BCG + threadIdx.x;
+  const int nthr = BCG * TL;
+  for (int i = tid; i < E * BC * S; i += nthr) {
+    const int e = i / (BC * S);
+    const int r = i - e * BC * S;
+    const int cl = r / S;
+    const int s = r - cl * S;
+    const int c = cs + cl;
+    lds[(e * S + s) * BC + cl] = c < g.C ? to_f32(beta[(int64_t(e) * g.C + c) * S + s]) : 0.f;
+  }
+  __syncthreads();
+  const int cl0 = threadIdx.x * V;
+  const int c0 = cs + cl0;
+  if (c0 >= g.C) return;
+  const int m_begin = chunk * tpb;
+  const int m_end = min(m_begin + tpb, g.M);
+  for (int m = m_begin + threadIdx.y; m < m_end; m += TL) {
+    const int64_t p0 = cell_pixel0(m, g, index);
+    float acc[S][V];
+    if (add_x) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) load_vec<TX, V>(x + slot_offset<K>(p0, s, g, c0), acc[s]);
+    } else {
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc[s][v] = 0.f;
+    }
+    const int64_t zoff = int64_t(m) * g.C + c0;
+    for (int e = 0; e < E; ++e) {
+      float dz[V];
+      load_vec<TW, V>(static_cast<const TW*>(upd.p[e]) + zoff, dz);
+      const float* b = lds + e * S * BC + cl0;
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc[s][v] = fmaf(b[s * BC + v], dz[v], acc[s][v]);
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) store_vec<TX, V>(out + slot_offset<K>(p0, s, g, c0), acc[s]);
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// Block reduction helper: sums W = (blockDim.x * NV) floats per thread over threadIdx.y
+// and hands each (lane-major) sum to `emit(i, value)`. red must hold TL * W floats.
+// ----------------------------------------------------------------------------------
+template <int NV, typename Emit>
+__device__ __forceinline__ void block_reduce_rows(const float* acc, float* red, Emit&& emit) {
+  const int W = blockDim.x * NV;
+  const int TL = blockDim.y;
+  const int tid = threadIdx.y * blockDim.x + threadIdx.x;
+  const int nthr = blockDim.x * TL;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) red[threadIdx.y * W + threadIdx.x * NV + v] = acc[v];
+  __syncthreads();
+  for (int i = tid; i < W; i += nthr) {
+    float sum = 0.f;
+    for (int ty = 0; ty < TL; ++ty) sum += red[ty * W + i];
+    emit(i, sum);
+  }
+  __syncthreads();
+}
+
+// ----------------------------------------------------------------------------------
+// weight gradient partials: part[chunk][e][s][c] = sum_{m in chunk} x[m,s,c] * z_e[m,c]
+// CARRIER: x is the NHWC carrier with S = K*K slots; otherwise x is a workspace
+// [M, C] tensor (S = 1; the triangular gamma gradient).
+// block (BCG*S lanes, lane = s*BCG + cg; TL), grid (slices, chunks).
+// ----------------------------------------------------------------------------------
+template <typename T, int V, int K, int EMAX, bool CARRIER>
+__global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack z,
+                                               float* __restrict__ part,
+                                               const int32_t* __restrict__ index, int E, int BCG,
+                                               Geo g, int tpb, int nslices) {
+  constexpr int S = CARRIER ? K * K : 1;
+  extern __shared__ float red[];
+  const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
+  const int s = threadIdx.x / BCG;
+  const int cg = threadIdx.x - s * BCG;
+  const int BC = BCG * V;
+  const int c0 = slice * BC + cg * V;
+  float acc[EMAX][V];
+#pragma unroll
+  for (int j = 0; j < EMAX; ++j)
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[j][v] = 0.f;
+  if (c0 < g.C) {
+    const int m_begin = chunk * tpb;
+    const int m_end = min(m_begin + tpb, g.M);
+    for (int m = m_begin + threadIdx.y; m < m_end; m += blockDim.y) {
+      int64_t xoff;
+      if constexpr (CARRIER) {
+        xoff = slot_offset<K>(cell_pixel0(m, g, index), s, g, c0);
+      } else {
+        xoff = int64_t(m) * g.C + c0;
+      }
+      float xv[V];
+      load_vec<T, V>(x + xoff, xv);
+      const int64_t zoff = int64_t(m) * g.C + c0;
+#pragma unroll
+      for (int j = 0; j < EMAX; ++j) {
+        if (j < E) {
+          float zv[V];
+          load_vec<T, V>(static_cast<const T*>(z.p[j]) + zoff, zv);
+#pragma unroll
+          for (int v = 0; v < V; ++v) acc[j][v] = fmaf(xv[v], zv[v], acc[j][v]);
+        }
+      }
+    }
+  }
+  float* prow = part + int64_t(chunk) * E * S * g.C;
+  const int cs = slice * BC;
+#pragma unroll
+  for (int j = 0; j < EMAX; ++j) {
+    if (j < E) {
+      block_reduce_rows<V>(acc[j], red, [&](int i, float sum) {
+        const int ss = i / BC;
+        const int c = cs + (i - ss * BC);
+        if (c < g.C) prow[(int64_t(j) * S + ss) * g.C + c] = sum;
+      });
+    }
+  }
+}
+
+// out[e][c][s] (TO) = sum_k part[k][e][s][c] in ascending k.
+template <typename TO>
+__global__ void __launch_bounds__(256) k_finalize(const float* __restrict__ part, TO* __restrict__ out,
+                                                  int chunks, int E, int S, int C) {
+  const int64_t n = int64_t(E) * S * C;
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int e = int(i / (int64_t(S) * C));
+  const int r = int(i - int64_t(e) * S * C);
+  const int s = r / C;
+  const int c = r - s * C;
+  float sum = 0.f;
+  for (int k = 0; k < chunks; ++k) sum += part[int64_t(k) * n + i];
+  out[(int64_t(e) * C + c) * S + s] = from_f32<TO>(sum);
+}
+
+// ----------------------------------------------------------------------------------
+// triangular: out[m,c] = base[m,c] + sum_j gamma[j,c] * upd_j[m,c]
+// ----------------------------------------------------------------------------------
+template <typename T, typename TG, int V>
+__global__ void __launch_bounds__(256) k_triangular(const T* __restrict__ base, PtrPack upd,
+                                                    const TG* __restrict__ gamma, T* __restrict__ out,
+                                                    int A, int M, int C, int tpb, int nslices) {
+  extern __shared__ float lds[];
+  const int BCG = blockDim.x, TL = blockDim.y;
+  const int BC = BCG * V;
+  const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
+  const int cs = slice * BC;
+  const int tid = threadIdx.y * BCG + threadIdx.x;
+  for (int i = tid; i < A * BC; i += BCG * TL) {
+    const int j = i / BC;
+    const int cl = i - j * BC;
+    const int c = cs + cl;
+    lds[i] = c < C ? to_f32(gamma[int64_t(j) * C + c]) : 0.f;
+  }
+  __syncthreads();
+  const int cl0 = threadIdx.x * V;
+  const int c0 = cs + cl0;
+  if (c0 >= C) return;
+  const int m_begin = chunk * tpb;
+  const int m_end = min(m_begin + tpb, M);
+  for (int m = m_begin + threadIdx.y; m < m_end; m += TL) {
+    const int64_t off = int64_t(m) * C + c0;
+    float acc[V];
+    load_vec<T, V>(base + off, acc);
+    for (int j = 0; j < A; ++j) {
+      float dz[V];
+      load_vec<T, V>(static_cast<const T*>(upd.p[j]) + off, dz);
+      const float* gm = lds + j * BC + cl0;
+#pragma unroll
+      for (int v = 0; v < V; ++v) acc[v] = fmaf(gm[v], dz[v], acc[v]);
+    }
+    store_vec<T, V>(out + off, acc);
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// per-event fused forward: x_out = x + beta*dz ; z_out = sum_s alpha_next * x_out
+// The single event's [C,S] weights of the lane's V channels live in registers.
+// ----------------------------------------------------------------------------------
+template <typename T, int V, int K>
+__device__ __forceinline__ void load_weights(const T* __restrict__ w, int c0, float (&out)[K * K][V]) {
+  constexpr int S = K * K;
+  float tmp[V * S];
+  load_vec<T, V * S>(w + int64_t(c0) * S, tmp);
+#pragma unroll
+  for (int v = 0; v < V; ++v)
+#pragma unroll
+    for (int s = 0; s < S; ++s) out[s][v] = tmp[v * S + s];
+}
+
+template <typename T, int V, int K>
+__global__ void __launch_bounds__(256) k_event_fwd(const T* __restrict__ x, const T* __restrict__ dz,
+                                                   const T* __restrict__ beta,
+                                                   const T* __restrict__ alpha, T* __restrict__ xo,
+                                                   T* __restrict__ zo, const int32_t* __restrict__ index,
+                                                   Geo g, int tpb, int nslices) {
+  constexpr int S = K * K;
+  const int BCG = blockDim.x, TL = blockDim.y;
+  const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
+  const int c0 = (slice * BCG + threadIdx.x) * V;
+  if (c0 >= g.C) return;
+  float bw[S][V], aw[S][V];
+  load_weights<T, V, K>(beta, c0, bw);
+  const bool has_z = alpha != nullptr;
+  if (has_z) load_weights<T, V, K>(alpha, c0, aw);
+  const int m_begin = chunk * tpb;
+  const int m_end = min(m_begin + tpb, g.M);
+  for (int m = m_begin + threadIdx.y; m < m_end; m += TL) {
+    const int64_t p0 = cell_pixel0(m, g, index);
+    const int64_t zoff = int64_t(m) * g.C + c0;
+    float d[V];
+    load_vec<T, V>(dz + zoff, d);
+    float xv[S][V];
+#pragma unroll
+    for (int s = 0; s < S; ++s) load_vec<T, V>(x + slot_offset<K>(p0, s, g, c0), xv[s]);
+    float zacc[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) zacc[v] = 0.f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) xv[s][v] = round_as<T>(fmaf(bw[s][v], d[v], xv[s][v]));
+      store_vec<T, V>(xo + slot_offset<K>(p0, s, g, c0), xv[s]);
+#pragma unroll
+      for (int v = 0; v < V; ++v) zacc[v] = fmaf(aw[s][v], xv[s][v], zacc[v]);
+    }
+    if (has_z) store_vec<T, V>(zo + zoff, zacc);
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// per-event fused backward (see sihc_event_backward in sihc_hip.h)
+// part[chunk][0][s][c] = partial grad_beta, part[chunk][1][s][c] = partial grad_alpha_next
+// ----------------------------------------------------------------------------------
+template <typename T, int V, int K>
+__global__ void __launch_bounds__(256) k_event_bwd(const T* __restrict__ gxo, const T* __restrict__ gzo,
+                                                   const T* __restrict__ xo, const T* __restrict__ dz,
+                                                   const T* __restrict__ beta,
+                                                   const T* __restrict__ alpha, T* __restrict__ gx,
+                                                   T* __restrict__ gdz, float* __restrict__ part,
+                                                   const int32_t* __restrict__ index, Geo g, int tpb, int nslices) {
+  constexpr int S = K * K;
+  extern __shared__ float red[];
+  const int BCG = blockDim.x, TL = blockDim.y;
+  const int BC = BCG * V;
+  const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
+  const int c0 = slice * BC + threadIdx.x * V;
+  const bool active = c0 < g.C;
+  const bool has_h = gxo != nullptr;
+  const bool has_g = gzo != nullptr;   // read part: t += alpha*gz, grad_alpha partials
+  const bool has_w = beta != nullptr;  // write part: grad_dz, grad_beta partials
+  const bool store_t = gx != nullptr;  // else t == grad_x_out and the caller aliases it
+  float bw[S][V], aw[S][V];
+  float db[S][V], da[S][V];
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      db[s][v] = 0.f;
+      da[s][v] = 0.f;
+      aw[s][v] = 0.f;
+      bw[s][v] = 0.f;
+    }
+  if (active) {
+    if (has_w) load_weights<T, V, K>(beta, c0, bw);
+    if (has_g) load_weights<T, V, K>(alpha, c0, aw);
+    const int m_begin = chunk * tpb;
+    const int m_end = min(m_begin + tpb, g.M);
+    for (int m = m_begin + threadIdx.y; m < m_end; m += TL) {
+      const int64_t p0 = cell_pixel0(m, g, index);
+      const int64_t zoff = int64_t(m) * g.C + c0;
+      float gz[V], d[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        gz[v] = 0.f;
+        d[v] = 0.f;
+      }
+      if (has_g) load_vec<T, V>(gzo + zoff, gz);
+      if (has_w) load_vec<T, V>(dz + zoff, d);
+      float gd[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) gd[v] = 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const int64_t off = slot_offset<K>(p0, s, g, c0);
+        float t[V];
+        if (has_h) {
+          load_vec<T, V>(gxo + off, t);
+        } else {
+#pragma unroll
+          for (int v = 0; v < V; ++v) t[v] = 0.f;
+        }
+        if (has_g) {
+          float xv[V];
+          load_vec<T, V>(xo + off, xv);
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            da[s][v] = fmaf(xv[v], gz[v], da[s][v]);
+            t[v] = fmaf(aw[s][v], gz[v], t[v]);
+          }
+        }
+        if (store_t) store_vec<T, V>(gx + off, t);
+        if (has_w) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            gd[v] = fmaf(bw[s][v], t[v], gd[v]);
+            db[s][v] = fmaf(d[v], t[v], db[s][v]);
+          }
+        }
+      }
+      if (has_w) store_vec<T, V>(gdz + zoff, gd);
+    }
+  }
+  // Block reduction of the two [S][V] accumulators; partial rows are [2][S][C].
+  float* prow = part + int64_t(chunk) * 2 * S * g.C;
+  const int cs = slice * BC;
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    float flat[S * V];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int v = 0; v < V; ++v) flat[s * V + v] = w == 0 ? db[s][v] : da[s][v];
+    // lane-major layout in `red`: [ty][lane][s][v]; remap to [s][c] on emit.
+    block_reduce_rows<S * V>(flat, red, [&](int i, float sum) {
+      const int lane = i / (S * V);
+      const int r = i - lane * S * V;
+      const int s = r / V;
+      const int v = r - s * V;
+      const int c = cs + lane * V + v;
+      if (c < g.C) prow[(int64_t(w) * S + s) * g.C + c] = sum;
+    });
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// gather / scatter of whole cells (bit-exact copies of CH-byte chunks)
+// cells[m][s][:] <-> x[pixel(index(m), s)][:]
+// ----------------------------------------------------------------------------------
+template <typename R, int K, bool GATHER>
+__global__ void __launch_bounds__(256) k_cells(const R* __restrict__ src, R* __restrict__ dst,
+                                               const int32_t* __restrict__ index, Geo g, int row_chunks) {
+  constexpr int S = K * K;
+  const int64_t row = int64_t(blockIdx.x) * blockDim.y + threadIdx.y;  // m*S + s
+  if (row >= int64_t(g.M) * S) return;
+  const int m = int(row / S);
+  const int s = int(row - int64_t(m) * S);
+  const int64_t pix = cell_pixel0(m, g, index) + int64_t(s / K) * g.GK + (s % K);
+  const int64_t xrow = pix * row_chunks;
+  const int64_t crow = row * row_chunks;
+  for (int i = threadIdx.x; i < row_chunks; i += blockDim.x) {
+    if constexpr (GATHER) {
+      dst[crow + i] = src[xrow + i];
+    } else {
+      dst[xrow + i] = src[crow + i];
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, int64_t n) {
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+
+__global__ void k_copy1(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = src[i];
+}
+
+// out0[c][s] = sum_k part[k][0][s][c]; out1[c][s] = sum_k part[k][1][s][c] (if out1).
+template <typename TO>
+__global__ void __launch_bounds__(256) k_finalize_pair(const float* __restrict__ part, TO* __restrict__ out0,
+                                                       TO* __restrict__ out1, int chunks, int S, int C) {
+  const int64_t n = int64_t(S) * C;
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= 2 * n) return;
+  const int w = int(i / n);
+  TO* out = w == 0 ? out0 : out1;
+  if (!out) return;
+  const int r = int(i - w * n);
+  const int s = r / C;
+  const int c = r - s * C;
+  float sum = 0.f;
+  for (int k = 0; k < chunks; ++k) sum += part[int64_t(k) * 2 * n + i];
+  out[int64_t(c) * S + s] = from_f32<TO>(sum);
+}
+
+// ==================================================================================
+// host side
+// ==================================================================================
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(SIHC_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(err));
+  return SIHC_OK;
+}
+
+int elem_size(int dtype) { return dtype == SIHC_DTYPE_F32 ? 4 : 2; }
+bool valid_dtype(int dtype) { return dtype == SIHC_DTYPE_F32 || dtype == SIHC_DTYPE_BF16; }
+
+bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % uintptr_t(bytes)) == 0; }
+
+// Largest V in {8, 4, 1} (V*elem <= max_bytes) such that C % V == 0 and every pointer
+// is aligned to V*elem bytes. `elem` is the widest element size among the tensors.
+int pick_vec(int C, int elem, int max_bytes, const void* const* ptrs, int n) {
+  for (int v : {8, 4}) {
+    if (v * elem > max_bytes || C % v) continue;
+    bool ok = true;
+    for (int i = 0; i < n && ok; ++i) ok = ptrs[i] == nullptr || aligned(ptrs[i], v * elem);
+    if (ok) return v;
+  }
+  return 1;
+}
+
+struct Shape2D {
+  int bcg, tl, slices;
+};
+
+// Channel groups per block: 16 lanes of V channels (a 256-byte run per token row for
+// 16-byte vectors), reduced when the weight slice would not fit `lds_cap` bytes.
+Shape2D shape_for(int C, int V, int lds_per_channel, int lds_cap = 64 * 1024) {
+  const int CG = (C + V - 1) / V;
+  int bcg = 16;
+  while (bcg > 1 && bcg / 2 >= CG) bcg /= 2;
+  while (bcg > 1 && int64_t(lds_per_channel) * bcg * V > lds_cap) bcg /= 2;
+  Shape2D sh;
+  sh.bcg = bcg;
+  sh.tl = 256 / bcg;
+  sh.slices = (CG + bcg - 1) / bcg;
+  return sh;
+}
+
+int chunk_count(int64_t M, int tokens_per_chunk, int max_chunks) {
+  int64_t n = (M + tokens_per_chunk - 1) / tokens_per_chunk;
+  if (n < 1) n = 1;
+  if (n > max_chunks) n = max_chunks;
+  return int(n);
+}
+// Token chunks of the weight-gradient reductions: a function of sizes only, so that
+// the workspace size query and the launch agree.
+int wgrad_chunks(int64_t M) { return chunk_count(M, 512, 128); }
+int event_bwd_chunks(int64_t M) { return chunk_count(M, 256, 256); }
+
+int check_geometry(const char* what, int64_t batch, int grid, int cell, int channels, Geo* g) {
+  if (batch < 0 || grid <= 0 || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
+  if (cell != 2 && cell != 4) return fail(SIHC_ERR_INVALID, "%s: cell must be 2 or 4 (4 or 16 slots)", what);
+  const int64_t M = batch * int64_t(grid) * grid;
+  const int64_t carrier = M * cell * cell * int64_t(channels);
+  if (M >= (int64_t(1) << 31) || carrier >= (int64_t(1) << 47))
+    return fail(SIHC_ERR_INVALID, "%s: tensor too large", what);
+  g->M = int(M);
+  g->GG = grid * grid;
+  g->G = grid;
+  g->K = cell;
+  g->GK = grid * cell;
+  g->C = channels;
+  return SIHC_OK;
+}
+
+int check_events(const char* what, int events, const void* const* ptrs) {
+  if (events < 1 || events > SIHC_MAX_EVENTS)
+    return fail(SIHC_ERR_INVALID, "%s: events must be in 1..%d, got %d", what, SIHC_MAX_EVENTS, events);
+  if (!ptrs) return fail(SIHC_ERR_INVALID, "%s: null pointer array", what);
+  for (int i = 0; i < events; ++i)
+    if (!ptrs[i]) return fail(SIHC_ERR_INVALID, "%s: null tensor pointer %d", what, i);
+  return SIHC_OK;
+}
+
+PtrPack pack(const void* const* ptrs, int n) {
+  PtrPack p;
+  std::memset(&p, 0, sizeof(p));
+  for (int i = 0; i < n; ++i) p.p[i] = ptrs[i];
+  return p;
+}
+
+template <typename F>
+int with_dtype(int dtype, F&& f) {
+  if (dtype == SIHC_DTYPE_F32) return f(float{});
+  return f(bf16_t{});
+}
+template <typename F>
+int with_vec(int v, F&& f) {
+  if (v == 8) return f(IC<8>{});
+  if (v == 4) return f(IC<4>{});
+  return f(IC<1>{});
+}
+template <typename F>
+int with_cell(int k, F&& f) {
+  if (k == 2) return f(IC<2>{});
+  return f(IC<4>{});
+}
+
+// 1-D grid of slices x chunks (slices fastest: concurrently resident blocks cover whole
+// channel rows of a token range).
+unsigned blocks1d(int slices, int64_t chunks) { return unsigned(int64_t(slices) * chunks); }
+
+int cells_copy(const char* what, bool gather, const void* src, const int32_t* index, void* dst, int64_t batch,
+               int grid, int cell, int channels, int dtype, void* stream) {
+  Geo g;
+  if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
+  if (!valid_dtype(dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype %d", what, dtype);
+  if (!src || !dst) return fail(SIHC_ERR_INVALID, "%s: null pointer", what);
+  if (g.M == 0) return SIHC_OK;
+  const int64_t row_bytes = int64_t(channels) * elem_size(dtype);
+  const int S = cell * cell;
+  const int64_t rows = int64_t(g.M) * S;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto go = [&](auto r) {
+    using R = decltype(r);
+    const int row_chunks = int(row_bytes / int64_t(sizeof(R)));
+    int bx = 64;
+    while (bx > 1 && bx / 2 >= row_chunks) bx /= 2;
+    const int by = 256 / bx;
+    const int64_t gx = (rows + by - 1) / by;
+    if (gx > 0x7fffffff) return fail(SIHC_ERR_INVALID, "%s: too many rows", what);
+    auto launch = [&](auto kk) {
+      constexpr int KK = decltype(kk)::value;
+      if (gather) {
+        hipLaunchKernelGGL((k_cells<R, KK, true>), dim3(unsigned(gx)), dim3(bx, by), 0, st,
+                           static_cast<const R*>(src), static_cast<R*>(dst), index, g, row_chunks);
+      } else {
+        hipLaunchKernelGGL((k_cells<R, KK, false>), dim3(unsigned(gx)), dim3(bx, by), 0, st,
+                           static_cast<const R*>(src), static_cast<R*>(dst), index, g, row_chunks);
+      }
+      return check_launch(what);
+    };
+    return with_cell(cell, launch);
+  };
+  if (row_bytes % 16 == 0 && aligned(src, 16) && aligned(dst, 16)) return go(uint4{});
+  if (row_bytes % 4 == 0 && aligned(src, 4) && aligned(dst, 4)) return go(uint32_t{});
+  return go(uint16_t{});
+}
+
+}  // namespace
+
+// ==================================================================================
+// C ABI
+// ==================================================================================
+extern "C" {
+
+const char* sihc_last_error(void) { return g_last_error.c_str(); }
+int sihc_abi_version(void) { return SIHC_ABI_VERSION; }
+
+int sihc_read(const void* x, const void* alpha, void* const* out, int events, int64_t batch, int grid,
+              int cell, int channels, const int32_t* index, int dtype, void* stream) {
+  const char* what = "sihc_read";
+  Geo g;
+  if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
+  if (!valid_dtype(dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype %d", what, dtype);
+  if (!x || !alpha) return fail(SIHC_ERR_INVALID, "%s: null input", what);
+  if (int rc = check_events(what, events, const_cast<const void* const*>(out))) return rc;
+  if (g.M == 0) return SIHC_OK;
+  const int es = elem_size(dtype);
+  const void* ptrs[SIHC_MAX_EVENTS + 1];
+  for (int i = 0; i < events; ++i) ptrs[i] = out[i];
+  ptrs[events] = x;
+  const int V = pick_vec(channels, es, 16, ptrs, events + 1);
+  const int S = cell * cell;
+  const Shape2D sh = shape_for(channels, V, events * S * 4);
+  const int tpb = sh.tl * 8;
+  const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
+  const size_t lds = size_t(events) * S * sh.bcg * V * 4;
+  const PtrPack pk = pack(ptrs, events);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_dtype(dtype, [&](auto t) {
+    using T = decltype(t);
+    return with_vec(V, [&](auto vv) {
+      constexpr int VV = decltype(vv)::value;
+      if constexpr (VV * sizeof(T) > 16) {
+        return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
+      } else {
+        return with_cell(cell, [&](auto kk) {
+          constexpr int KK = decltype(kk)::value;
+          hipLaunchKernelGGL((k_read<T, VV, KK>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), lds, st,
+                             static_cast<const T*>(x), static_cast<const T*>(alpha), pk, index, events, g, tpb, sh.slices);
+          return check_launch(what);
+        });
+      }
+    });
+  });
+}
+
+int sihc_write(const void* x, const void* const* updates, const void* beta, void* out, int events,
+               int64_t batch, int grid, int cell, int channels, int add_x, const int32_t* index, int x_dtype,
+               int w_dtype, void* stream) {
+  const char* what = "sihc_write";
+  Geo g;
+  if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
+  if (!valid_dtype(x_dtype) || !valid_dtype(w_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
+  if (x_dtype == SIHC_DTYPE_BF16 && w_dtype == SIHC_DTYPE_F32)
+    return fail(SIHC_ERR_INVALID, "%s: fp32 updates with a bf16 carrier are not supported", what);
+  if ((add_x && !x) || !beta || !out) return fail(SIHC_ERR_INVALID, "%s: null input", what);
+  if (int rc = check_events(what, events, updates)) return rc;
+  if (g.M == 0) return SIHC_OK;
+  const void* ptrs[SIHC_MAX_EVENTS + 2];
+  for (int i = 0; i < events; ++i) ptrs[i] = updates[i];
+  ptrs[events] = add_x ? x : nullptr;
+  ptrs[events + 1] = out;
+  const int es = std::max(elem_size(x_dtype), elem_size(w_dtype));
+  const int V = pick_vec(channels, es, 16, ptrs, events + 2);
+  const int S = cell * cell;
+  const Shape2D sh = shape_for(channels, V, events * S * 4);
+  const int tpb = sh.tl * 8;
+  const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
+  const size_t lds = size_t(events) * S * sh.bcg * V * 4;
+  const PtrPack pk = pack(updates, events);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto launch = [&](auto tx, auto tw) {
+    using TX = decltype(tx);
+    using TW = decltype(tw);
+    return with_vec(V, [&](auto vv) {
+      constexpr int VV = decltype(vv)::value;
+      if constexpr (VV * sizeof(TX) > 16) {
+        return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
+      } else {
+        return with_cell(cell, [&](auto kk) {
+          constexpr int KK = decltype(kk)::value;
+          hipLaunchKernelGGL((k_write<TX, TW, VV, KK>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), lds,
+                             st, static_cast<const TX*>(x), pk, static_cast<const TW*>(beta), static_cast<TX*>(out),
+                             index, events, add_x ? 1 : 0, g, tpb, sh.slices);
+          return check_launch(what);
+        });
+      }
+    });
+  };
+  if (x_dtype == SIHC_DTYPE_F32 && w_dtype == SIHC_DTYPE_F32) return launch(float{}, float{});
+  if (x_dtype == SIHC_DTYPE_F32) return launch(float{}, bf16_t{});
+  return launch(bf16_t{}, bf16_t{});
+}
+
+size_t sihc_weight_grad_workspace_size(int events, int64_t batch, int grid, int cell, int channels) {
+  if (events < 1 || batch < 0 || grid <= 0 || cell <= 0 || channels <= 0) return 0;
+  const int64_t M = batch * int64_t(grid) * grid;
+  return size_t(wgrad_chunks(M)) * events * cell * cell * channels * sizeof(float);
+}
+
+namespace {
+// Shared launcher of the atomics-free weight-gradient reduction + finalize.
+int launch_wgrad(const char* what, const void* x, const void* const* z, void* out, int events, const Geo& g,
+                 int S, bool carrier, const int32_t* index, int dtype, int out_dtype, void* workspace,
+                 size_t workspace_bytes, hipStream_t st) {
+  const int chunks = wgrad_chunks(g.M);
+  const size_t need = size_t(chunks) * events * S * g.C * sizeof(float);
+  if (!workspace || workspace_bytes < need)
+    return fail(SIHC_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", what, need, workspace_bytes);
+  if (!aligned(workspace, 16)) return fail(SIHC_ERR_INVALID, "%s: workspace must be 16-byte aligned", what);
+  const int es = elem_size(dtype);
+  const void* ptrs[SIHC_MAX_EVENTS + 1];
+  for (int i = 0; i < events; ++i) ptrs[i] = z[i];
+  ptrs[events] = x;
+  const int emax = events <= 8 ? 8 : events <= 16 ? 16 : 32;
+  // Keep <= 128 fp32 accumulators per lane: 8 channels up to 16 events, else 4.
+  const int vmax_bytes = emax == 32 ? 4 * es : 16;
+  const int V = pick_vec(g.C, es, vmax_bytes, ptrs, events + 1);
+  const int CG = (g.C + V - 1) / V;
+  int bcg = 16;
+  while (bcg > 1 && bcg / 2 >= CG) bcg /= 2;
+  while (bcg * S > 256) bcg /= 2;
+  const int lanes = bcg * S;
+  const int tl = 256 / lanes;
+  const int slices = (CG + bcg - 1) / bcg;
+  const int tpb = int((int64_t(g.M) + chunks - 1) / chunks);
+  const size_t lds = size_t(tl) * lanes * V * sizeof(float);
+  const PtrPack pk = pack(z, events);
+  float* part = static_cast<float*>(workspace);
+  int rc = with_dtype(dtype, [&](auto t) {
+    using T = decltype(t);
+    return with_vec(V, [&](auto vv) {
+      constexpr int VV = decltype(vv)::value;
+      if constexpr (VV * sizeof(T) > 16) {
+        return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
+      } else {
+        auto go = [&](auto em, auto kk, auto car) {
+          constexpr int EM = decltype(em)::value;
+          constexpr int KK = decltype(kk)::value;
+          constexpr bool CAR = decltype(car)::value != 0;
+          if constexpr (EM * VV > 128) {
+            return fail(SIHC_ERR_INVALID, "%s: internal accumulator width", what);
+          } else {
+            hipLaunchKernelGGL((k_wgrad<T, VV, KK, EM, CAR>), dim3(blocks1d(slices, chunks)), dim3(lanes, tl), lds, st,
+                               static_cast<const T*>(x), pk, part, index, events, bcg, g, tpb, slices);
+            return check_launch(what);
+          }
+        };
+        auto with_em = [&](auto kk, auto car) {
+          if (emax == 8) return go(IC<8>{}, kk, car);
+          if (emax == 16) return go(IC<16>{}, kk, car);
+          return go(IC<32>{}, kk, car);
+        };
+        if (!carrier) return with_em(IC<2>{}, IC<0>{});
+        if (g.K == 2) return with_em(IC<2>{}, IC<1>{});
+        return with_em(IC<4>{}, IC<1>{});
+      }
+    });
+  });
+  if (rc) return rc;
+  const int64_t n = int64_t(events) * S * g.C;
+  const unsigned blocks = unsigned((n + 255) / 256);
+  if (out_dtype == SIHC_DTYPE_F32) {
+    hipLaunchKernelGGL((k_finalize<float>), dim3(blocks), dim3(256), 0, st, part, static_cast<float*>(out), chunks,
+                       events, S, g.C);
+  } else {
+    hipLaunchKernelGGL((k_finalize<bf16_t>), dim3(blocks), dim3(256), 0, st, part, static_cast<bf16_t*>(out),
+                       chunks, events, S, g.C);
+  }
+  return check_launch(what);
+}
+}  // namespace
+
+int sihc_weight_grad(const void* x, const void* const* z, void* out, int events, int64_t batch, int grid, int cell,
+                     int channels, const int32_t* index, int dtype, int out_dtype, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  const char* what = "sihc_weight_grad";
+  Geo g;
+  if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
+  if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
+  if (!x || !out) return fail(SIHC_ERR_INVALID, "%s: null input", what);
+  if (int rc = check_events(what, events, z)) return rc;
+  if (g.M == 0) {
+    // Empty reduction: zero gradient.
+    hipError_t e = hipMemsetAsync(out, 0, size_t(events) * cell * cell * channels * elem_size(out_dtype),
+                                  static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? SIHC_OK : fail(SIHC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  }
+  return launch_wgrad(what, x, z, out, events, g, cell * cell, true, index, dtype, out_dtype, workspace,
+                      workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int sihc_triangular(const void* base, const void* const* updates, const void* gamma, void* out, int active,
+                    int64_t rows, int channels, int dtype, int gamma_dtype, void* stream) {
+  const char* what = "sihc_triangular";
+  if (rows < 0 || rows >= (int64_t(1) << 31) || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
+  if (!valid_dtype(dtype) || !valid_dtype(gamma_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
+  if (!base || !gamma || !out) return fail(SIHC_ERR_INVALID, "%s: null input", what);
+  if (int rc = check_events(what, active, updates)) return rc;
+  if (rows == 0) return SIHC_OK;
+  const int es = elem_size(dtype);
+  const void* ptrs[SIHC_MAX_EVENTS + 2];
+  for (int i = 0; i < active; ++i) ptrs[i] = updates[i];
+  ptrs[active] = base;
+  ptrs[active + 1] = out;
+  const int V = pick_vec(channels, es, 16, ptrs, active + 2);
+  const Shape2D sh = shape_for(channels, V, active * 4);
+  const int tpb = sh.tl * 8;
+  const int64_t chunks = (rows + tpb - 1) / tpb;
+  const size_t lds = size_t(active) * sh.bcg * V * 4;
+  const PtrPack pk = pack(updates, active);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_dtype(dtype, [&](auto t) {
+    using T = decltype(t);
+    return with_dtype(gamma_dtype, [&](auto tg) {
+      using TG = decltype(tg);
+      return with_vec(V, [&](auto vv) {
+        constexpr int VV = decltype(vv)::value;
+        if constexpr (VV * sizeof(T) > 16) {
+          return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
+        } else {
+          hipLaunchKernelGGL((k_triangular<T, TG, VV>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), lds,
+                             st, static_cast<const T*>(base), pk, static_cast<const TG*>(gamma), static_cast<T*>(out),
+                             active, int(rows), channels, tpb, sh.slices);
+          return check_launch(what);
+        }
+      });
+    });
+  });
+}
+
+size_t sihc_triangular_gamma_grad_workspace_size(int active, int64_t rows, int channels) {
+  if (active < 1 || rows < 0 || channels <= 0) return 0;
+  return size_t(wgrad_chunks(rows)) * active * channels * sizeof(float);
+}
+
+int sihc_triangular_gamma_grad(const void* grad, const void* const* updates, void* out, int active, int64_t rows,
+                               int channels, int dtype, int out_dtype, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  const char* what = "sihc_triangular_gamma_grad";
+  if (rows < 0 || rows >= (int64_t(1) << 31) || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
+  if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
+  if (!grad || !out) return fail(SIHC_ERR_INVALID, "%s: null input", what);
+  if (int rc = check_events(what, active, updates)) return rc;
+  if (rows == 0) {
+    hipError_t e = hipMemsetAsync(out, 0, size_t(active) * channels * elem_size(out_dtype),
+                                  static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? SIHC_OK : fail(SIHC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  }
+  Geo g;
+  g.M = int(rows);
+  g.GG = 1;
+  g.G = 1;
+  g.K = 1;
+  g.GK = 1;
+  g.C = channels;
+  return launch_wgrad(what, grad, updates, out, active, g, 1, false, nullptr, dtype, out_dtype, workspace,
+                      workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+namespace {
+// Vector width of the per-event kernels: registers hold 2*S*V weights (and, backward,
+// 2*S*V accumulators), so wide vectors are used only for the 4-slot cell.
+int event_vec(int C, int es, int cell, const void* const* ptrs, int n) {
+  return pick_vec(C, es, cell == 2 ? 16 : 2 * es, ptrs, n);
+}
+}  // namespace
+
+int sihc_event_forward(const void* x, const void* dz, const void* beta, const void* alpha_next, void* x_out,
+                       void* z_out, int64_t batch, int grid, int cell, int channels, const int32_t* index, int dtype,
+                       void* stream) {
+  const char* what = "sihc_event_forward";
+  Geo g;
+  if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
+  if (!valid_dtype(dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
+  if (!x || !dz || !beta || !x_out) return fail(SIHC_ERR_INVALID, "%s: null input", what);
+  if ((alpha_next == nullptr) != (z_out == nullptr))
+    return fail(SIHC_ERR_INVALID, "%s: alpha_next and z_out must both be given or both be NULL", what);
+  if (g.M == 0) return SIHC_OK;
+  const int es = elem_size(dtype);
+  const int S = cell * cell;
+  const void* ptrs[] = {x, dz, x_out, z_out};
+  if (!aligned(beta, std::min(16, S * es)) || (alpha_next && !aligned(alpha_next, std::min(16, S * es))))
+    return fail(SIHC_ERR_INVALID, "%s: weights must be aligned to %d bytes", what, std::min(16, S * es));
+  int V = event_vec(channels, es, cell, ptrs, 4);
+  // Weight rows are loaded as V*S contiguous elements: need V*S*es alignment.
+  while (V > 1 && (!aligned(beta, V * S * es) || (alpha_next && !aligned(alpha_next, V * S * es)))) V = V == 8 ? 4 : 1;
+  const Shape2D sh = shape_for(channels, V, 0);
+  const int tpb = sh.tl * 8;
+  const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_dtype(dtype, [&](auto t) {
+    using T = decltype(t);
+    return with_vec(V, [&](auto vv) {
+      constexpr int VV = decltype(vv)::value;
+      if constexpr (VV * sizeof(T) > 16) {
+        return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
+      } else {
+        return with_cell(cell, [&](auto kk) {
+          constexpr int KK = decltype(kk)::value;
+          if constexpr (KK == 4 && VV > 2) {
+            return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
+          } else {
+            hipLaunchKernelGGL((k_event_fwd<T, VV, KK>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), 0, st,
+                               static_cast<const T*>(x), static_cast<const T*>(dz), static_cast<const T*>(beta),
+                               static_cast<const T*>(alpha_next), static_cast<T*>(x_out), static_cast<T*>(z_out),
+                               index, g, tpb, sh.slices);
+            return check_launch(what);
+          }
+        });
+      }
+    });
+  });
+}
+
+size_t sihc_event_backward_workspace_size(int64_t batch, int grid, int cell, int channels) {
+  if (batch < 0 || grid <= 0 || cell <= 0 || channels <= 0) return 0;
+  const int64_t M = batch * int64_t(grid) * grid;
+  return size_t(event_bwd_chunks(M)) * 2 * cell * cell * channels * sizeof(float);
+}
+
+int sihc_event_backward(const void* grad_x_out, const void* grad_z_out, const void* x_out, const void* dz,
+                        const void* beta, const void* alpha_next, void* grad_x, void* grad_dz, void* grad_beta,
+                        void* grad_alpha_next, int64_t batch, int grid, int cell, int channels,
+                        const int32_t* index, int dtype, int w_dtype, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  const char* what = "sihc_event_backward";
+  Geo g;
+  if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
+  if (!valid_dtype(dtype) || !valid_dtype(w_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
+  const bool has_w = beta != nullptr;
+  if (has_w != (dz != nullptr) || has_w != (grad_dz != nullptr) || has_w != (grad_beta != nullptr))
+    return fail(SIHC_ERR_INVALID, "%s: beta, dz, grad_dz and grad_beta must all be given or all be NULL", what);
+  if (grad_z_out && (!alpha_next || !x_out || !grad_alpha_next))
+    return fail(SIHC_ERR_INVALID, "%s: grad_z_out needs alpha_next, x_out and grad_alpha_next", what);
+  if (!has_w && !grad_z_out) return fail(SIHC_ERR_INVALID, "%s: neither a write nor a read part", what);
+  if (!grad_x && grad_z_out)
+    return fail(SIHC_ERR_INVALID, "%s: grad_x may be NULL only without grad_z_out (it equals grad_x_out)", what);
+  const int S = cell * cell;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (g.M == 0) {
+    hipError_t e = has_w ? hipMemsetAsync(grad_beta, 0, size_t(S) * channels * elem_size(w_dtype), st) : hipSuccess;
+    if (e == hipSuccess && grad_alpha_next)
+      e = hipMemsetAsync(grad_alpha_next, 0, size_t(S) * channels * elem_size(w_dtype), st);
+    return e == hipSuccess ? SIHC_OK : fail(SIHC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  }
+  const int chunks = event_bwd_chunks(g.M);
+  const size_t need = size_t(chunks) * 2 * S * channels * sizeof(float);
+  if (!workspace || workspace_bytes < need)
+    return fail(SIHC_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", what, need, workspace_bytes);
+  if (!aligned(workspace, 16)) return fail(SIHC_ERR_INVALID, "%s: workspace must be 16-byte aligned", what);
+  const int es = elem_size(dtype);
+  const void* ptrs[] = {grad_x_out, grad_z_out, x_out, dz, grad_x, grad_dz};
+  if ((beta && !aligned(beta, std::min(16, S * es))) || (alpha_next && !aligned(alpha_next, std::min(16, S * es))))
+    return fail(SIHC_ERR_INVALID, "%s: weights must be aligned to %d bytes", what, std::min(16, S * es));
+  int V = event_vec(channels, es, cell, ptrs, 6);
+  while (V > 1 && (!aligned(beta, V * S * es) || (grad_z_out && !aligned(alpha_next, V * S * es)))) V = V == 8 ? 4 : 1;
+  const Shape2D sh = shape_for(channels, V, 0);
+  const int tpb = int((int64_t(g.M) + chunks - 1) / chunks);
+  const size_t lds = size_t(sh.tl) * sh.bcg * S * V * sizeof(float);  // TL x (BCG*S*V) floats
+  float* part = static_cast<float*>(workspace);
+  int rc = with_dtype(dtype, [&](auto t) {
+    using T = decltype(t);
+    return with_vec(V, [&](auto vv) {
+      constexpr int VV = decltype(vv)::value;
+      if constexpr (VV * sizeof(T) > 16) {
+        return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
+      } else {
+        return with_cell(cell, [&](auto kk) {
+          constexpr int KK = decltype(kk)::value;
+          if constexpr (KK == 4 && VV > 2) {
+            return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
+          } else {
+            hipLaunchKernelGGL((k_event_bwd<T, VV, KK>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), lds, st,
+                               static_cast<const T*>(grad_x_out), static_cast<const T*>(grad_z_out),
+                               static_cast<const T*>(x_out), static_cast<const T*>(dz), static_cast<const T*>(beta),
+                               static_cast<const T*>(alpha_next), static_cast<T*>(grad_x), static_cast<T*>(grad_dz),
+                               part, index, g, tpb, sh.slices);
+            return check_launch(what);
+          }
+        });
+      }
+    });
+  });
+  if (rc) return rc;
+  // Partial rows are [chunks][2][S][C]: row 0 -> grad_beta, row 1 -> grad_alpha_next.
+  const int64_t n = int64_t(S) * channels;
+  const unsigned blocks = unsigned((2 * n + 255) / 256);
+  void* gan = grad_z_out ? grad_alpha_next : nullptr;
+  if (w_dtype == SIHC_DTYPE_F32) {
+    hipLaunchKernelGGL((k_finalize_pair<float>), dim3(blocks), dim3(256), 0, st, part, static_cast<float*>(grad_beta),
+                       static_cast<float*>(gan), chunks, S, channels);
+  } else {
+    hipLaunchKernelGGL((k_finalize_pair<bf16_t>), dim3(blocks), dim3(256), 0, st, part,
+                       static_cast<bf16_t*>(grad_beta), static_cast<bf16_t*>(gan), chunks, S, channels);
+  }
+  if (int rc2 = check_launch(what)) return rc2;
+  if (grad_alpha_next && !grad_z_out) {
+    hipError_t e = hipMemsetAsync(grad_alpha_next, 0, size_t(n) * elem_size(w_dtype), st);
+    if (e != hipSuccess) return fail(SIHC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  }
+  return SIHC_OK;
+}
+
+int sihc_gather_cells(const void* x, const int32_t* index, void* cells, int64_t batch, int grid, int cell,
+                      int channels, int dtype, void* stream) {
+  return cells_copy("sihc_gather_cells", true, x, index, cells, batch, grid, cell, channels, dtype, stream);
+}
+
+int sihc_scatter_cells(const void* cells, const int32_t* index, void* x, int64_t batch, int grid, int cell,
+                       int channels, int dtype, void* stream) {
+  return cells_copy("sihc_scatter_cells", false, cells, index, x, batch, grid, cell, channels, dtype, stream);
+}
+
+int sihc_copy(const void* src, void* dst, size_t bytes, void* stream) {
+  const char* what = "sihc_copy";
+  if (bytes == 0) return SIHC_OK;
+  if (!src || !dst) return fail(SIHC_ERR_INVALID, "%s: null pointer", what);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (aligned(src, 16) && aligned(dst, 16) && bytes % 16 == 0) {
+    const int64_t n = int64_t(bytes / 16);
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 256 * 64) blocks = 256 * 64;
+    hipLaunchKernelGGL(k_copy16, dim3(unsigned(blocks)), dim3(256), 0, st, static_cast<const uint4*>(src),
+                       static_cast<uint4*>(dst), n);
+  } else {
+    const int64_t n = int64_t(bytes);
+    hipLaunchKernelGGL(k_copy1, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, static_cast<const uint8_t*>(src),
+                       static_cast<uint8_t*>(dst), n);
+  }
+  return check_launch(what);
+}
+
+}  // extern "C"

@@ -1,0 +1,93 @@
+"""CPU: the C-ABI library loads, exports every declared symbol, and rejects bad
+arguments before any launch (no kernel runs here)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from sihc_hip import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "sihc_hip.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(sihc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = declared_functions()
+    assert len(names) >= 14, names
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in sihc_hip.h but not exported"
+    # ... and the ctypes prototypes cover exactly the header.
+    assert set(names) == set(_lib.PROTOTYPES), set(names) ^ set(_lib.PROTOTYPES)
+    assert lib.sihc_abi_version() == _lib.ABI_VERSION
+
+
+def test_workspace_sizes_are_pure_functions_of_sizes():
+    lib = _lib.lib()
+    # 65,536 tokens (batch 256 of a 16x16 grid), 24 events, 4 slots, 1152 channels.
+    ws = lib.sihc_weight_grad_workspace_size(24, 256, 16, 2, 1152)
+    assert ws == 128 * 24 * 4 * 1152 * 4
+    assert lib.sihc_weight_grad_workspace_size(0, 256, 16, 2, 1152) == 0
+    assert lib.sihc_triangular_gamma_grad_workspace_size(3, 147, 67) == 1 * 3 * 67 * 4
+    assert lib.sihc_event_backward_workspace_size(256, 16, 2, 1152) == 256 * 2 * 4 * 1152 * 4
+
+
+FAKE = 0x1000  # never dereferenced: every call below fails argument validation first
+
+
+@pytest.mark.parametrize("events", [0, 33])
+def test_event_count_is_validated_before_launch(events):
+    lib = _lib.lib()
+    outs = _lib.ptr_array([FAKE] * max(events, 1))
+    rc = lib.sihc_read(FAKE, FAKE, outs, events, 2, 16, 2, 64, None, _lib.DTYPE_BF16, None)
+    assert rc == 1
+    assert b"events must be in 1..32" in lib.sihc_last_error()
+
+
+def test_bad_cell_dtype_and_null_pointers_are_rejected():
+    lib = _lib.lib()
+    outs = _lib.ptr_array([FAKE])
+    assert lib.sihc_read(FAKE, FAKE, outs, 1, 2, 16, 3, 64, None, _lib.DTYPE_BF16, None) == 1
+    assert b"cell must be 2 or 4" in lib.sihc_last_error()
+    assert lib.sihc_read(FAKE, FAKE, outs, 1, 2, 16, 2, 64, None, 7, None) == 1
+    assert b"bad dtype" in lib.sihc_last_error()
+    assert lib.sihc_read(None, FAKE, outs, 1, 2, 16, 2, 64, None, _lib.DTYPE_BF16, None) == 1
+    assert b"null" in lib.sihc_last_error()
+    nulls = _lib.ptr_array([FAKE, None])
+    assert lib.sihc_write(FAKE, nulls, FAKE, FAKE, 2, 2, 16, 2, 64, 1, None, 1, 1, None) == 1
+    assert b"null tensor pointer 1" in lib.sihc_last_error()
+    assert lib.sihc_write(FAKE, outs, FAKE, FAKE, 1, 2, 16, 2, 64, 1, None,
+                          _lib.DTYPE_BF16, _lib.DTYPE_F32, None) == 1
+    assert lib.sihc_event_forward(FAKE, FAKE, FAKE, FAKE, FAKE, None, 2, 16, 2, 64, None, 1, None) == 1
+    assert b"alpha_next and z_out" in lib.sihc_last_error()
+
+
+def test_too_small_workspace_is_rejected():
+    lib = _lib.lib()
+    ups = _lib.ptr_array([FAKE])
+    rc = lib.sihc_weight_grad(FAKE, ups, FAKE, 1, 256, 16, 2, 1152, None, 1, 1, FAKE, 16, None)
+    assert rc == 1 and b"workspace of" in lib.sihc_last_error()
+    rc = lib.sihc_event_backward(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                 256, 16, 2, 1152, None, 1, 1, FAKE, 16, None)
+    assert rc == 1 and b"workspace of" in lib.sihc_last_error()
+
+
+def test_oversized_tensor_is_rejected():
+    lib = _lib.lib()
+    outs = _lib.ptr_array([FAKE])
+    assert lib.sihc_read(FAKE, FAKE, outs, 1, 1 << 40, 16, 2, 64, None, 1, None) == 1
+    assert b"too large" in lib.sihc_last_error()
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libsihc_hip.so")
+    with pytest.raises(RuntimeError, match="missing"):
+        _lib.lib()

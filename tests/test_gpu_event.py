@@ -1,0 +1,105 @@
+"""GPU parity of the per-event fused write+read (literal schedule) and its adjoint."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from helpers import announce, assert_parity
+from oracle import sihc_oracle as O
+from sihc_hip import launch
+from sihc_hip.event_ops import event_write_read, literal_stage
+
+pytestmark = pytest.mark.gpu
+DTYPES = [torch.float32, torch.bfloat16]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("slots", [4, 16])
+@pytest.mark.parametrize("channels", [67, 64])
+def test_event_forward_matches_write_then_read(dtype, slots, channels):
+    announce(f"event fwd dtype={dtype} slots={slots} C={channels}")
+    torch.manual_seed(11)
+    k = O.cell_edge(slots)
+    x = torch.randn(3, 7 * k, 7 * k, channels, device="cuda", dtype=dtype)
+    dz = torch.randn(3, 49, channels, device="cuda", dtype=dtype)
+    beta = (1.0 + 0.02 * torch.randn(channels, slots, device="cuda")).to(dtype)
+    alpha = (0.25 + 0.02 * torch.randn(channels, slots, device="cuda")).to(dtype)
+    x_out, z_out = launch.event_forward(x, dz, beta, alpha)
+    rx, rz = O.event_forward(x.cpu(), dz.cpu(), beta.cpu(), alpha.cpu())
+    assert_parity(x_out, rx, dtype, what="x_out")
+    assert_parity(z_out, rz, dtype, what="z_out")
+    # the write half is the E=1 stage write, bit for bit
+    assert torch.equal(x_out, launch.write(x, [dz], beta[None]))
+    x_only, none = launch.event_forward(x, dz, beta, None)
+    assert none is None and torch.equal(x_only, x_out)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("slots", [4, 16])
+@pytest.mark.parametrize("has_h,has_g", [(True, True), (False, True), (True, False)])
+def test_event_backward_matches_adjoint(dtype, slots, has_h, has_g):
+    announce(f"event bwd dtype={dtype} slots={slots} h={has_h} g={has_g}")
+    torch.manual_seed(12)
+    k = O.cell_edge(slots)
+    c = 72
+    x_out = torch.randn(4, 9 * k, 9 * k, c, device="cuda", dtype=dtype)
+    dz = torch.randn(4, 81, c, device="cuda", dtype=dtype)
+    beta = (1.0 + 0.02 * torch.randn(c, slots, device="cuda")).to(dtype)
+    alpha = (0.25 + 0.02 * torch.randn(c, slots, device="cuda")).to(dtype)
+    h = (1e-2 * torch.randn_like(x_out)) if has_h else None
+    g = (1e-2 * torch.randn_like(dz)) if has_g else None
+    gx, gdz, gb, ga = launch.event_backward(h, g, x_out, dz, beta, alpha)
+    ref = O.event_backward(None if h is None else h.cpu(), None if g is None else g.cpu(), x_out.cpu(),
+                           dz.cpu(), beta.cpu(), alpha.cpu())
+    assert_parity(gx, ref[0], dtype, what="grad_x")
+    assert_parity(gdz, ref[1], dtype, what="grad_dz")
+    assert_parity(gb, ref[2], dtype, what="grad_beta")
+    if has_g:
+        assert_parity(ga, ref[3], dtype, what="grad_alpha_next")
+    else:
+        assert torch.count_nonzero(ga) == 0
+    # deterministic reductions
+    again = launch.event_backward(h, g, x_out, dz, beta, alpha)
+    for a, b in zip((gx, gdz, gb, ga), again):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("slots", [4, 16])
+def test_literal_stage_forward_and_gradients(dtype, slots):
+    # Literal per-event schedule on HIP vs the oracle's literal schedule
+    # (fusion_controls.py:41-85, "literal") with autograd through both.
+    announce(f"literal stage dtype={dtype} slots={slots}")
+    torch.manual_seed(21)
+    k = O.cell_edge(slots)
+    events, c = 6, 40
+    x = torch.randn(2, 5 * k, 5 * k, c, device="cuda", dtype=dtype).requires_grad_()
+    alpha = (0.25 + 0.05 * torch.randn(events, c, slots, device="cuda")).to(dtype).requires_grad_()
+    beta = (1.0 + 0.05 * torch.randn(events, c, slots, device="cuda")).to(dtype).requires_grad_()
+    fns = [lambda z, i=i: 0.1 * torch.tanh((1 + 0.1 * i) * z) for i in range(events)]
+    out = literal_stage(x, alpha, beta, fns)
+    go = torch.randn_like(out) * 0.1
+    grads = torch.autograd.grad(out, (x, alpha, beta), go)
+    xc, ac, bc = (t.detach().cpu().clone().requires_grad_() for t in (x, alpha, beta))
+    ref = O.literal_stage(xc, ac, bc, fns)
+    rgrads = torch.autograd.grad(ref, (xc, ac, bc), go.cpu())
+    assert_parity(out, ref, dtype, what="carrier")
+    for name, a, b in zip(("dX", "dalpha", "dbeta"), grads, rgrads):
+        assert_parity(a, b, dtype, what=name)
+
+
+def test_event_op_handles_unused_outputs():
+    announce("event op unused outputs")
+    torch.manual_seed(3)
+    x = torch.randn(2, 8, 8, 32, device="cuda", requires_grad=True)
+    dz = torch.randn(2, 16, 32, device="cuda", requires_grad=True)
+    beta = torch.randn(32, 4, device="cuda", requires_grad=True)
+    alpha = torch.randn(32, 4, device="cuda", requires_grad=True)
+    x_out, z_out = event_write_read(x, dz, beta, alpha)
+    gx, gdz, gb, ga = torch.autograd.grad(z_out.sum(), (x, dz, beta, alpha))
+    ref = O.event_backward(None, torch.ones(2, 16, 32), x_out.detach().cpu(), dz.detach().cpu(),
+                           beta.detach().cpu(), alpha.detach().cpu())
+    for a, b in zip((gx, gdz, gb, ga), ref):
+        assert_parity(a, b, torch.float32)
+    gx2, = torch.autograd.grad(x_out.sum(), (x,))
+    assert torch.equal(gx2, torch.ones_like(gx2))

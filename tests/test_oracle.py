@@ -1,0 +1,173 @@
+"""CPU: pin the oracle before trusting it (no GPU, no product code).
+
+Each check is chosen so that a plausible oracle mistake (swapped slot order, a
+transposed weight, a dropped term, a wrong adjoint) fails at least one of them.
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sihc_oracle as O
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _load(name):
+    return dict(np.load(GOLDEN / f"{name}.npz", allow_pickle=False))
+
+
+def test_known_answer_slot_order_and_round_trip():
+    # Reference known answer: research/tests/test_reference_variants.py:85-94.
+    high = torch.arange(32 * 32, dtype=torch.float32).reshape(1, 32, 32, 1)
+    cells = O.high_to_cells(high, 4)
+    assert cells.shape == (1, 256, 4, 1)
+    assert cells[0, 0, :, 0].tolist() == [0.0, 1.0, 32.0, 33.0]
+    assert torch.equal(O.cells_to_high(cells), high)
+    # p4 (16 slots): first cell is rows 0..3, cols 0..3 of a 64-wide carrier.
+    high4 = torch.arange(64 * 64, dtype=torch.float32).reshape(1, 64, 64, 1)
+    c4 = O.high_to_cells(high4, 16)
+    assert c4[0, 0, :, 0].tolist() == [r * 64 + c for r in range(4) for c in range(4)]
+    assert torch.equal(O.cells_to_high(c4), high4)
+
+
+def test_carrier_offset_matches_cell_layout():
+    # The brute-force index map agrees with the reshape/permute layout on every element.
+    x = torch.arange(2 * 6 * 6 * 3, dtype=torch.float64).reshape(2, 6, 6, 3)
+    cells = O.high_to_cells(x, 4)
+    for m in range(2 * 9):
+        for s in range(4):
+            for c in range(3):
+                assert O.carrier_offset(m, s, c, 3, 3, 2) == int(cells[m // 9, m % 9, s, c])
+
+
+@pytest.mark.parametrize("name", ["p8_small", "p4_small"])
+def test_torch_restatement_matches_brute_force_fixtures(name):
+    f = _load(name)
+    x = torch.from_numpy(f["x"]).double()
+    alpha = torch.from_numpy(f["alpha"]).double()
+    beta = torch.from_numpy(f["beta"]).double()
+    updates = [torch.from_numpy(u).double() for u in f["updates"]]
+    slots = alpha.shape[2]
+    got = torch.stack(O.read(x, alpha))
+    torch.testing.assert_close(got, torch.from_numpy(f["read"]), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(O.write(x, updates, beta), torch.from_numpy(f["write"]), rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(O.write(x, updates, beta, add_x=False), torch.from_numpy(f["write_noadd"]),
+                               rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(O.weight_grad(x, updates, slots).double(), torch.from_numpy(f["weight_grad"]),
+                               rtol=1e-6, atol=1e-6)
+    gamma = torch.from_numpy(f["gamma"]).double()
+    torch.testing.assert_close(O.triangular_torch(updates[0], updates[1:], gamma[1:]),
+                               torch.from_numpy(f["triangular"]), rtol=1e-12, atol=1e-12)
+    index = torch.from_numpy(f["index"])
+    assert torch.equal(O.gather_cells(torch.from_numpy(f["x"]), index, slots), torch.from_numpy(f["gather"]))
+
+
+@pytest.mark.parametrize("slots", [4, 16])
+def test_read_write_are_adjoint(slots):
+    torch.manual_seed(1)
+    k = O.cell_edge(slots)
+    x = torch.randn(2, 5 * k, 5 * k, 7, dtype=torch.float64)
+    alpha = torch.randn(3, 7, slots, dtype=torch.float64)
+    g = [torch.randn(2, 25, 7, dtype=torch.float64) for _ in range(3)]
+    lhs = sum((z * gi).sum() for z, gi in zip(O.read(x, alpha), g))
+    rhs = (x * O.write(x, g, alpha, add_x=False)).sum()
+    torch.testing.assert_close(lhs, rhs, rtol=1e-12, atol=1e-12)
+
+
+def test_identity_initialised_stage_is_the_residual_recurrence():
+    # Reference: research/tests/test_reference_variants.py:97-123.
+    torch.manual_seed(0)
+    high = torch.randn(2, 32, 32, 5, dtype=torch.float64)
+    alpha = torch.full((3, 5, 4), 0.25, dtype=torch.float64)
+    beta = torch.ones(3, 5, 4, dtype=torch.float64)
+    fns = [lambda z, s=s: torch.tanh(z * s) for s in (0.1, 0.2, 0.3)]
+    actual = O.fused_stage(high, alpha, beta, fns)
+    cells = O.high_to_cells(high, 4)
+    z = cells.mean(dim=2)
+    ups = []
+    for fn in fns:
+        u = fn(z)
+        ups.append(u)
+        z = z + u
+    expected = O.cells_to_high(cells + torch.stack(ups).sum(0).unsqueeze(2))
+    torch.testing.assert_close(actual, expected)
+
+
+@pytest.mark.parametrize("slots", [4, 16])
+def test_literal_recurrence_equals_fused_stage(slots):
+    # Late materialisation (README.md:36-51) is exact algebra: check it in float64.
+    torch.manual_seed(5)
+    k = O.cell_edge(slots)
+    x = torch.randn(2, 4 * k, 4 * k, 6, dtype=torch.float64)
+    alpha = 0.3 * torch.randn(6, 6, slots, dtype=torch.float64)
+    beta = 0.3 * torch.randn(6, 6, slots, dtype=torch.float64)
+    fns = [lambda z, i=i: torch.tanh((i + 1) * 0.1 * z) for i in range(6)]
+    torch.testing.assert_close(O.literal_stage(x, alpha, beta, fns), O.fused_stage(x, alpha, beta, fns),
+                               rtol=1e-10, atol=1e-10)
+
+
+def test_weight_gradients_match_autograd():
+    torch.manual_seed(2)
+    x = torch.randn(2, 8, 8, 3, dtype=torch.float64, requires_grad=True)
+    alpha = torch.randn(2, 3, 4, dtype=torch.float64, requires_grad=True)
+    g = [torch.randn(2, 16, 3, dtype=torch.float64) for _ in range(2)]
+    loss = sum((z * gi).sum() for z, gi in zip(O.read(x, alpha), g))
+    dx, da = torch.autograd.grad(loss, (x, alpha))
+    torch.testing.assert_close(O.weight_grad(x.detach(), g, 4).double(), da, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(O.write(x.detach(), g, alpha.detach(), add_x=False), dx)
+    # triangular gamma gradient == autograd of triangular_torch
+    base = torch.randn(2, 16, 3, dtype=torch.float64)
+    ups = [torch.randn(2, 16, 3, dtype=torch.float64) for _ in range(3)]
+    gamma = torch.randn(3, 3, dtype=torch.float64, requires_grad=True)
+    go = torch.randn(2, 16, 3, dtype=torch.float64)
+    (dg,) = torch.autograd.grad((O.triangular_torch(base, ups, gamma) * go).sum(), (gamma,))
+    torch.testing.assert_close(O.triangular_gamma_grad(go, ups).double(), dg, rtol=1e-6, atol=1e-6)
+
+
+def test_event_backward_matches_autograd():
+    torch.manual_seed(3)
+    x = torch.randn(2, 6, 6, 4, dtype=torch.float64, requires_grad=True)
+    dz = torch.randn(2, 9, 4, dtype=torch.float64, requires_grad=True)
+    beta = torch.randn(4, 4, dtype=torch.float64, requires_grad=True)
+    alpha = torch.randn(4, 4, dtype=torch.float64, requires_grad=True)
+    x_out, z_out = O.event_forward(x, dz, beta, alpha)
+    h = torch.randn_like(x_out)
+    g = torch.randn_like(z_out)
+    grads = torch.autograd.grad((x_out * h).sum() + (z_out * g).sum(), (x, dz, beta, alpha))
+    mine = O.event_backward(h, g, x_out.detach(), dz.detach(), beta.detach(), alpha.detach())
+    for a, b in zip(mine, grads):
+        torch.testing.assert_close(a, b)
+
+
+def test_gather_scatter_round_trip_and_identity():
+    torch.manual_seed(4)
+    x = torch.randn(3, 8, 8, 5)
+    idx = torch.stack([torch.randperm(16) for _ in range(3)]).to(torch.int32)
+    cells = O.gather_cells(x, idx, 4)
+    assert torch.equal(O.scatter_cells(cells, idx), x)
+    ident = torch.arange(16, dtype=torch.int32).expand(3, 16).contiguous()
+    assert torch.equal(O.gather_cells(x, ident, 4), O.high_to_cells(x, 4))
+
+
+def test_planted_slot_swap_is_caught(monkeypatch):
+    """A mistake planted in the oracle (slots ux/uy transposed) must fail the pins."""
+    def swapped(x, slots):
+        b, h, w, c = x.shape
+        k = O.cell_edge(slots)
+        g = h // k
+        return x.reshape(b, g, k, g, k, c).permute(0, 1, 3, 4, 2, 5).reshape(b, g * g, k * k, c)
+
+    monkeypatch.setattr(O, "high_to_cells", swapped)
+    with pytest.raises(AssertionError):
+        test_known_answer_slot_order_and_round_trip()
+    # ... and the weight-gradient fixture (weights indexed by slot) disagrees too.
+    f = _load("p8_small")
+    x = torch.from_numpy(f["x"]).double()
+    ups = [torch.from_numpy(u).double() for u in f["updates"]]
+    with pytest.raises(AssertionError):
+        torch.testing.assert_close(O.weight_grad(x, ups, 4).double(), torch.from_numpy(f["weight_grad"]),
+                                   rtol=1e-6, atol=1e-6)
