@@ -50,6 +50,9 @@ def parse_args():
     p.add_argument("--seed", type=int, default=2)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    p.add_argument("--mode", choices=("step", "calibrate"), default="step",
+                   help="step: the benchmark (default); calibrate: a 1 GiB copy-kernel launch plus single "
+                        "event forward/backward launches at the same shape, for HBM counter runs")
     return p.parse_args()
 
 
@@ -215,6 +218,41 @@ def traffic_from_profiles() -> float | None:
         return None
 
 
+def calibrate(args) -> None:
+    """Launches for rocprofv3 counter runs: the library's copy kernel over a known byte
+    count (the FETCH_SIZE/WRITE_SIZE scale), then one per-event forward and one full
+    per-event backward at the benchmark shape, 3 times each."""
+    import torch
+
+    step = LiteralStep(args.batch, args.channels, 2, args.seed)
+    L, check = step.L, step.check
+    copy_bytes = 1 << 30
+    src = torch.empty(copy_bytes, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    torch.cuda.synchronize()
+    fwd = next(c for c in step.fwd if c[0] == "event_forward")
+    for _ in range(3):
+        check(L.sihc_copy(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), copy_bytes, step.stream))
+    # full backward of event 0 (reads grad of x_1 and z_1, x_1, dz_0; writes grad_x_0, grad_dz_0)
+    vp = ctypes.c_void_p
+    p = lambda t: vp(t.data_ptr())  # noqa: E731
+    B, G, K, C = step.B, step.G, step.K, step.C
+    bwd_args = (p(step.h_out), p(step.gz[1]), p(step.x[1]), p(step.dz[0]), p(step.beta[0]), p(step.alpha[1]),
+                p(step.gx[0]), p(step.gdz[0]), p(step.gbeta[0]), p(step.galpha[1]), B, G, K, C, None, 1, 1,
+                p(step.work), step.work.numel() * 4, step.stream)
+    for _ in range(3):
+        check(fwd[1](*fwd[2]))
+    for _ in range(3):
+        check(L.sihc_event_backward(*bwd_args))
+    torch.cuda.synchronize()
+    U = step.M * C * ELEM
+    print(json.dumps({"copy_bytes_read": copy_bytes, "copy_bytes_written": copy_bytes,
+                      "event_forward_bytes": fwd[3], "event_backward_bytes": 15 * U + 4 * C * 4 * ELEM,
+                      "event_forward_read": 5 * U, "event_forward_written": 5 * U,
+                      "event_backward_read": 10 * U, "event_backward_written": 5 * U}), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -227,6 +265,9 @@ def main():
         print("bench.py needs a GPU (MI355X); none is visible", file=sys.stderr)
         sys.exit(1)
     torch.cuda.set_device(0)
+    if args.mode == "calibrate":
+        calibrate(args)
+        return
     print(f"[bench] building step: batch={args.batch} C={args.channels} events={args.events}", file=sys.stderr,
           flush=True)
     step = LiteralStep(args.batch, args.channels, args.events, args.seed)

@@ -5,14 +5,16 @@
 // matrix-core work: per element the path does at most 2*E*S flops per 2*(S+E) bytes.
 //
 // Thread mapping shared by every kernel: a block is (BCG channel groups) x (TL token
-// lanes). A lane owns V adjacent channels (one 16-byte vector for bf16 V=8 / fp32 V=4)
-// and walks a run of tokens with stride TL, so each wave issues fully coalesced
-// 16-byte loads and the per-channel weights of its channel group are fetched once per
-// block: into LDS when the kernel handles many events (read / write / triangular), into
-// registers when it handles one (per-event fused kernels). All sums are fp32 with a
-// single round-to-nearest-even per stored element. Reductions over tokens (weight
-// gradients) are per-thread fp32 partials, then one LDS pass per block that writes a
-// per-block partial row, then a fixed-order sum over blocks: no atomics, deterministic.
+// lanes). A lane owns V adjacent channels (up to one 16-byte vector) and walks a run of
+// tokens with stride TL, so each wave issues fully coalesced vector loads, and the
+// per-channel weights of its channel group are fetched once per block: into LDS when
+// the kernel handles many events (read / write / triangular), into registers when it
+// handles one (per-event fused kernels). Every token is processed as "issue all loads,
+// then compute, then store" with no data-dependent branches in the loop body, so each
+// lane keeps all of a token's loads in flight at once. All sums are fp32 with a single
+// round-to-nearest-even per stored element. Reductions over tokens (weight gradients)
+// are per-lane fp32 partials, then one LDS pass per block that writes a per-block
+// partial row, then a fixed-order sum over blocks: no atomics, bitwise deterministic.
 //
 // Reference (behaviour, not code): tongtongliang/residual-stream-burden,
 // sihc/models/sihc/sublayer_kernels.py (Triton `_read`, `_write`, `_weight_grad`,
@@ -29,6 +31,41 @@
 #include <type_traits>
 
 #include "sihc_hip.h"
+
+// Launch-shape defaults (compile-time constants of the library).
+#ifndef SIHC_EV_VEC  // max channels per lane in the per-event kernels (4-slot cells)
+#define SIHC_EV_VEC 4
+#endif
+#ifndef SIHC_EV_BCG  // channel-group lanes per block, per-event kernels
+#define SIHC_EV_BCG 32
+#endif
+#ifndef SIHC_EV_TPT  // tokens per lane, per-event forward
+#define SIHC_EV_TPT 4
+#endif
+#ifndef SIHC_EV_UNROLL  // tokens per lane per loop iteration, per-event kernels
+#define SIHC_EV_UNROLL 2
+#endif
+#ifndef SIHC_EV_MINW  // occupancy hint (min waves per SIMD) of the per-event kernels
+#define SIHC_EV_MINW 1
+#endif
+#ifndef SIHC_EV_CHUNK  // tokens per reduction chunk, per-event backward
+#define SIHC_EV_CHUNK 256
+#endif
+#ifndef SIHC_RW_BCG  // channel-group lanes per block, read / write / triangular
+#define SIHC_RW_BCG 16
+#endif
+#ifndef SIHC_RW_TPT  // tokens per lane, read / write / triangular
+#define SIHC_RW_TPT 8
+#endif
+#ifndef SIHC_WG_CHUNK  // tokens per reduction chunk, weight / gamma gradients
+#define SIHC_WG_CHUNK 512
+#endif
+#ifndef SIHC_NT  // 1: non-temporal (streaming) hints on carrier/workspace traffic
+#define SIHC_NT 0
+#endif
+#ifndef SIHC_LOAD_FENCE  // 1: keep each token's loads ahead of its arithmetic (see load_fence)
+#define SIHC_LOAD_FENCE 1
+#endif
 
 namespace {
 
@@ -56,6 +93,16 @@ __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return bf16_t(u >> 16);
 }
+// Scheduling fence between a token's load phase and its arithmetic. Without it the
+// compiler interleaves loads with the math that consumes them to save registers,
+// leaving only two or three loads per lane in flight; with it every load of the
+// token is issued before the first wait.
+__device__ __forceinline__ void load_fence() {
+#if SIHC_LOAD_FENCE
+  __builtin_amdgcn_sched_barrier(0);
+#endif
+}
+
 // Value of v after a round trip through T (what a stored-then-reloaded element holds).
 template <typename T>
 __device__ __forceinline__ float round_as(float v) { return to_f32(from_f32<T>(v)); }
@@ -63,11 +110,30 @@ __device__ __forceinline__ float round_as(float v) { return to_f32(from_f32<T>(v
 // ----------------------------------------------------------------------------------
 // vector load/store of V elements of T as fp32
 // ----------------------------------------------------------------------------------
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 template <int BYTES> struct RawT;
-template <> struct RawT<16> { using type = uint4; };
-template <> struct RawT<8> { using type = uint2; };
+template <> struct RawT<16> { using type = u32x4; };
+template <> struct RawT<8> { using type = u32x2; };
 template <> struct RawT<4> { using type = uint32_t; };
 template <> struct RawT<2> { using type = uint16_t; };
+
+template <typename R>
+__device__ __forceinline__ R ld(const R* p) {
+#if SIHC_NT
+  return __builtin_nontemporal_load(p);
+#else
+  return *p;
+#endif
+}
+template <typename R>
+__device__ __forceinline__ void st(R* p, R v) {
+#if SIHC_NT
+  __builtin_nontemporal_store(v, p);
+#else
+  *p = v;
+#endif
+}
 
 template <typename T, int V>
 __device__ __forceinline__ void load_vec(const T* __restrict__ p, float* o) {
@@ -77,7 +143,7 @@ __device__ __forceinline__ void load_vec(const T* __restrict__ p, float* o) {
   using R = typename RawT<CH>::type;
 #pragma unroll
   for (int q = 0; q < BYTES / CH; ++q) {
-    R r = reinterpret_cast<const R*>(p)[q];
+    R r = ld(reinterpret_cast<const R*>(p) + q);
     T e[EPC];
     __builtin_memcpy(e, &r, CH);
 #pragma unroll
@@ -98,7 +164,24 @@ __device__ __forceinline__ void store_vec(T* __restrict__ p, const float* v) {
     for (int i = 0; i < EPC; ++i) e[i] = from_f32<T>(v[q * EPC + i]);
     R r;
     __builtin_memcpy(&r, e, CH);
-    reinterpret_cast<R*>(p)[q] = r;
+    st(reinterpret_cast<R*>(p) + q, r);
+  }
+}
+
+// Weights are tiny and reused by every block: plain cached loads.
+template <typename T, int V>
+__device__ __forceinline__ void load_vec_cached(const T* __restrict__ p, float* o) {
+  constexpr int BYTES = V * int(sizeof(T));
+  constexpr int CH = BYTES >= 16 ? 16 : BYTES;
+  constexpr int EPC = CH / int(sizeof(T));
+  using R = typename RawT<CH>::type;
+#pragma unroll
+  for (int q = 0; q < BYTES / CH; ++q) {
+    R r = reinterpret_cast<const R*>(p)[q];
+    T e[EPC];
+    __builtin_memcpy(e, &r, CH);
+#pragma unroll
+    for (int i = 0; i < EPC; ++i) o[q * EPC + i] = to_f32(e[i]);
   }
 }
 
@@ -137,9 +220,27 @@ __device__ __forceinline__ int64_t slot_offset(int64_t pix0, int s, const Geo& g
   return (pix0 + int64_t(s / K) * g.GK + (s % K)) * g.C + c;
 }
 
+// Stage a [E, C, S] weight stack's channel slice [cs, cs+BC) into LDS as [Epad][S][BC]
+// fp32, zero-filling padded events (e >= E) and channels past C.
+template <typename TW>
+__device__ __forceinline__ void stage_weights(float* lds, const TW* __restrict__ w, int E, int Epad, int S, int BC,
+                                              int cs, int C) {
+  const int tid = threadIdx.y * blockDim.x + threadIdx.x;
+  const int nthr = blockDim.x * blockDim.y;
+  for (int i = tid; i < Epad * BC * S; i += nthr) {  // global [e][c][s] -> LDS [e][s][c]
+    const int e = i / (BC * S);
+    const int r = i - e * BC * S;
+    const int cl = r / S;
+    const int s = r - cl * S;
+    const int c = cs + cl;
+    lds[(e * S + s) * BC + cl] = (e < E && c < C) ? to_f32(w[(int64_t(e) * C + c) * S + s]) : 0.f;
+  }
+  __syncthreads();
+}
+
 // ----------------------------------------------------------------------------------
 // read: out_e[m,c] = sum_s alpha[e,c,s] * x[m,s,c]
-// grid (slices, token chunks), block (BCG, TL); LDS holds alpha as [E][S][BC] fp32.
+// 1-D grid of (slices x chunks), block (BCG, TL); LDS holds alpha as [E][S][BC] fp32.
 // ----------------------------------------------------------------------------------
 template <typename T, int V, int K>
 __global__ void __launch_bounds__(256) k_read(const T* __restrict__ x, const T* __restrict__ alpha,
@@ -151,17 +252,7 @@ __global__ void __launch_bounds__(256) k_read(const T* __restrict__ x, const T* 
   const int BC = BCG * V;
   const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
   const int cs = slice * BC;
-  const int tid = threadIdx.y * BCG + threadIdx.x;
-  const int nthr = BCG * TL;
-  for (int i = tid; i < E * BC * S; i += nthr) {  // global [e][c][s] -> LDS [e][s][c]
-    const int e = i / (BC * S);
-    const int r = i - e * BC * S;
-    const int cl = r / S;
-    const int s = r - cl * S;
-    const int c = cs + cl;
-    lds[(e * S + s) * BC + cl] = c < g.C ? to_f32(alpha[(int64_t(e) * g.C + c) * S + s]) : 0.f;
-  }
-  __syncthreads();
+  stage_weights(lds, alpha, E, E, S, BC, cs, g.C);
   const int cl0 = threadIdx.x * V;
   const int c0 = cs + cl0;
   if (c0 >= g.C) return;
@@ -172,6 +263,7 @@ __global__ void __launch_bounds__(256) k_read(const T* __restrict__ x, const T* 
     float xv[S][V];
 #pragma unroll
     for (int s = 0; s < S; ++s) load_vec<T, V>(x + slot_offset<K>(p0, s, g, c0), xv[s]);
+    load_fence();
     const int64_t zoff = int64_t(m) * g.C + c0;
     for (int e = 0; e < E; ++e) {
       const float* a = lds + e * S * BC + cl0;
@@ -189,29 +281,22 @@ __global__ void __launch_bounds__(256) k_read(const T* __restrict__ x, const T* 
 
 // ----------------------------------------------------------------------------------
 // write: out[m,s,c] = (add_x ? x : 0) + sum_e beta[e,c,s] * upd_e[m,c]
+// Events are consumed in groups of 4 (E padded to a multiple of 4 with zero weights
+// and a repeated valid pointer), so each group's 4 update loads issue together.
 // ----------------------------------------------------------------------------------
-template <typename TX, typename TW, int V, int K>
+template <typename TX, typename TW, int V, int K, bool ADD_X>
 __global__ void __launch_bounds__(256) k_write(const TX* __restrict__ x, PtrPack upd,
                                                const TW* __restrict__ beta, TX* __restrict__ out,
-                                               const int32_t* __restrict__ index, int E, int add_x,
-                                               Geo g, int tpb, int nslices) {
+                                               const int32_t* __restrict__ index, int E, Geo g, int tpb,
+                                               int nslices) {
   constexpr int S = K * K;
   extern __shared__ float lds[];
   const int BCG = blockDim.x, TL = blockDim.y;
   const int BC = BCG * V;
   const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
   const int cs = slice * BC;
-  const int tid = threadIdx.y * BCG + threadIdx.x;
-  const int nthr = BCG * TL;
-  for (int i = tid; i < E * BC * S; i += nthr) {
-    const int e = i / (BC * S);
-    const int r = i - e * BC * S;
-    const int cl = r / S;
-    const int s = r - cl * S;
-    const int c = cs + cl;
-    lds[(e * S + s) * BC + cl] = c < g.C ? to_f32(beta[(int64_t(e) * g.C + c) * S + s]) : 0.f;
-  }
-  __syncthreads();
+  const int E4 = (E + 3) & ~3;
+  stage_weights(lds, beta, E, E4, S, BC, cs, g.C);
   const int cl0 = threadIdx.x * V;
   const int c0 = cs + cl0;
   if (c0 >= g.C) return;
@@ -219,8 +304,9 @@ __global__ void __launch_bounds__(256) k_write(const TX* __restrict__ x, PtrPack
   const int m_end = min(m_begin + tpb, g.M);
   for (int m = m_begin + threadIdx.y; m < m_end; m += TL) {
     const int64_t p0 = cell_pixel0(m, g, index);
+    const int64_t zoff = int64_t(m) * g.C + c0;
     float acc[S][V];
-    if (add_x) {
+    if constexpr (ADD_X) {
 #pragma unroll
       for (int s = 0; s < S; ++s) load_vec<TX, V>(x + slot_offset<K>(p0, s, g, c0), acc[s]);
     } else {
@@ -229,15 +315,19 @@ __global__ void __launch_bounds__(256) k_write(const TX* __restrict__ x, PtrPack
 #pragma unroll
         for (int v = 0; v < V; ++v) acc[s][v] = 0.f;
     }
-    const int64_t zoff = int64_t(m) * g.C + c0;
-    for (int e = 0; e < E; ++e) {
-      float dz[V];
-      load_vec<TW, V>(static_cast<const TW*>(upd.p[e]) + zoff, dz);
-      const float* b = lds + e * S * BC + cl0;
+    for (int e = 0; e < E4; e += 4) {
+      float dz[4][V];
 #pragma unroll
-      for (int s = 0; s < S; ++s)
+      for (int q = 0; q < 4; ++q) load_vec<TW, V>(static_cast<const TW*>(upd.p[e + q]) + zoff, dz[q]);
+      load_fence();
 #pragma unroll
-        for (int v = 0; v < V; ++v) acc[s][v] = fmaf(b[s * BC + v], dz[v], acc[s][v]);
+      for (int q = 0; q < 4; ++q) {
+        const float* b = lds + (e + q) * S * BC + cl0;
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+          for (int v = 0; v < V; ++v) acc[s][v] = fmaf(b[s * BC + v], dz[q][v], acc[s][v]);
+      }
     }
 #pragma unroll
     for (int s = 0; s < S; ++s) store_vec<TX, V>(out + slot_offset<K>(p0, s, g, c0), acc[s]);
@@ -268,8 +358,10 @@ __device__ __forceinline__ void block_reduce_rows(const float* acc, float* red, 
 // ----------------------------------------------------------------------------------
 // weight gradient partials: part[chunk][e][s][c] = sum_{m in chunk} x[m,s,c] * z_e[m,c]
 // CARRIER: x is the NHWC carrier with S = K*K slots; otherwise x is a workspace
-// [M, C] tensor (S = 1; the triangular gamma gradient).
-// block (BCG*S lanes, lane = s*BCG + cg; TL), grid (slices, chunks).
+// [M, C] tensor (S = 1; the triangular gamma gradient). EMAX events are accumulated
+// per lane; the host pads z.p[E..EMAX) with a valid pointer and only rows e < E are
+// reduced, so the token loop has no branches.
+// block (BCG*S lanes, lane = s*BCG + cg; TL), 1-D grid (slices x chunks).
 // ----------------------------------------------------------------------------------
 template <typename T, int V, int K, int EMAX, bool CARRIER>
 __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack z,
@@ -298,18 +390,16 @@ __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack 
       } else {
         xoff = int64_t(m) * g.C + c0;
       }
+      const int64_t zoff = int64_t(m) * g.C + c0;
       float xv[V];
       load_vec<T, V>(x + xoff, xv);
-      const int64_t zoff = int64_t(m) * g.C + c0;
+      float zv[EMAX][V];
 #pragma unroll
-      for (int j = 0; j < EMAX; ++j) {
-        if (j < E) {
-          float zv[V];
-          load_vec<T, V>(static_cast<const T*>(z.p[j]) + zoff, zv);
+      for (int j = 0; j < EMAX; ++j) load_vec<T, V>(static_cast<const T*>(z.p[j]) + zoff, zv[j]);
 #pragma unroll
-          for (int v = 0; v < V; ++v) acc[j][v] = fmaf(xv[v], zv[v], acc[j][v]);
-        }
-      }
+      for (int j = 0; j < EMAX; ++j)
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc[j][v] = fmaf(xv[v], zv[j][v], acc[j][v]);
     }
   }
   float* prow = part + int64_t(chunk) * E * S * g.C;
@@ -326,24 +416,60 @@ __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack 
   }
 }
 
-// out[e][c][s] (TO) = sum_k part[k][e][s][c] in ascending k.
+// ----------------------------------------------------------------------------------
+// Fixed-order sum of partial rows. part is [chunks][R][S][C]; row r of the result
+// goes to out0 + r*C*S ([R][C][S], `pair` == 0) or, with `pair`, row 0 -> out0 and
+// row 1 -> out1 (each [C][S]). Rows whose bit is set in zero_mask are written as
+// zeros without reading partials; a NULL destination row is skipped.
+// Block: 32 outputs x 8 chunk groups; each group sums its chunks in ascending order,
+// then the 8 group sums are added in ascending group order.
+// ----------------------------------------------------------------------------------
 template <typename TO>
-__global__ void __launch_bounds__(256) k_finalize(const float* __restrict__ part, TO* __restrict__ out,
-                                                  int chunks, int E, int S, int C) {
-  const int64_t n = int64_t(E) * S * C;
-  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const int e = int(i / (int64_t(S) * C));
-  const int r = int(i - int64_t(e) * S * C);
-  const int s = r / C;
-  const int c = r - s * C;
+__global__ void __launch_bounds__(256) k_finalize(const float* __restrict__ part, TO* __restrict__ out0,
+                                                  TO* __restrict__ out1, int chunks, int R, int S, int C,
+                                                  int pair, int zero_mask) {
+  constexpr int FO = 32, FG = 8;
+  __shared__ float red[FG][FO];
+  const int64_t n = int64_t(R) * S * C;
+  const int o = threadIdx.x % FO, grp = threadIdx.x / FO;
+  const int64_t i = int64_t(blockIdx.x) * FO + o;
+  const int r = i < n ? int(i / (int64_t(S) * C)) : 0;
+  const bool zero = (zero_mask >> r) & 1;
   float sum = 0.f;
-  for (int k = 0; k < chunks; ++k) sum += part[int64_t(k) * n + i];
-  out[(int64_t(e) * C + c) * S + s] = from_f32<TO>(sum);
+  if (i < n && !zero) {
+    // 8 independent loads in flight per thread; the sum order stays ascending in k.
+    int k = grp;
+    for (; k + 7 * FG < chunks; k += 8 * FG) {
+      float v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = part[int64_t(k + q * FG) * n + i];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) sum += v[q];
+    }
+    for (; k < chunks; k += FG) sum += part[int64_t(k) * n + i];
+  }
+  red[grp][o] = sum;
+  __syncthreads();
+  if (grp != 0 || i >= n) return;
+  float t = 0.f;
+#pragma unroll
+  for (int q = 0; q < FG; ++q) t += red[q][o];
+  const int rem = int(i - int64_t(r) * S * C);
+  const int s = rem / C;
+  const int c = rem - s * C;
+  TO* dst = pair ? (r == 0 ? out0 : out1) : (out0 ? out0 + int64_t(r) * C * S : nullptr);
+  if (dst) dst[int64_t(c) * S + s] = from_f32<TO>(zero ? 0.f : t);
+}
+
+template <typename TO>
+__global__ void __launch_bounds__(256) k_fill_zero(TO* __restrict__ out, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = from_f32<TO>(0.f);
 }
 
 // ----------------------------------------------------------------------------------
 // triangular: out[m,c] = base[m,c] + sum_j gamma[j,c] * upd_j[m,c]
+// (active count padded to a multiple of 4 with zero gamma rows, as in k_write)
 // ----------------------------------------------------------------------------------
 template <typename T, typename TG, int V>
 __global__ void __launch_bounds__(256) k_triangular(const T* __restrict__ base, PtrPack upd,
@@ -354,12 +480,13 @@ __global__ void __launch_bounds__(256) k_triangular(const T* __restrict__ base, 
   const int BC = BCG * V;
   const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
   const int cs = slice * BC;
+  const int A4 = (A + 3) & ~3;
   const int tid = threadIdx.y * BCG + threadIdx.x;
-  for (int i = tid; i < A * BC; i += BCG * TL) {
+  for (int i = tid; i < A4 * BC; i += BCG * TL) {
     const int j = i / BC;
     const int cl = i - j * BC;
     const int c = cs + cl;
-    lds[i] = c < C ? to_f32(gamma[int64_t(j) * C + c]) : 0.f;
+    lds[i] = (j < A && c < C) ? to_f32(gamma[int64_t(j) * C + c]) : 0.f;
   }
   __syncthreads();
   const int cl0 = threadIdx.x * V;
@@ -371,12 +498,17 @@ __global__ void __launch_bounds__(256) k_triangular(const T* __restrict__ base, 
     const int64_t off = int64_t(m) * C + c0;
     float acc[V];
     load_vec<T, V>(base + off, acc);
-    for (int j = 0; j < A; ++j) {
-      float dz[V];
-      load_vec<T, V>(static_cast<const T*>(upd.p[j]) + off, dz);
-      const float* gm = lds + j * BC + cl0;
+    for (int j = 0; j < A4; j += 4) {
+      float dz[4][V];
 #pragma unroll
-      for (int v = 0; v < V; ++v) acc[v] = fmaf(gm[v], dz[v], acc[v]);
+      for (int q = 0; q < 4; ++q) load_vec<T, V>(static_cast<const T*>(upd.p[j + q]) + off, dz[q]);
+      load_fence();
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float* gm = lds + (j + q) * BC + cl0;
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc[v] = fmaf(gm[v], dz[q][v], acc[v]);
+      }
     }
     store_vec<T, V>(out + off, acc);
   }
@@ -390,76 +522,87 @@ template <typename T, int V, int K>
 __device__ __forceinline__ void load_weights(const T* __restrict__ w, int c0, float (&out)[K * K][V]) {
   constexpr int S = K * K;
   float tmp[V * S];
-  load_vec<T, V * S>(w + int64_t(c0) * S, tmp);
+  load_vec_cached<T, V * S>(w + int64_t(c0) * S, tmp);
 #pragma unroll
   for (int v = 0; v < V; ++v)
 #pragma unroll
     for (int s = 0; s < S; ++s) out[s][v] = tmp[v * S + s];
 }
 
-template <typename T, int V, int K>
-__global__ void __launch_bounds__(256) k_event_fwd(const T* __restrict__ x, const T* __restrict__ dz,
+template <typename T, int V, int K, bool HAS_Z>
+__global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_fwd(const T* __restrict__ x, const T* __restrict__ dz,
                                                    const T* __restrict__ beta,
                                                    const T* __restrict__ alpha, T* __restrict__ xo,
                                                    T* __restrict__ zo, const int32_t* __restrict__ index,
                                                    Geo g, int tpb, int nslices) {
   constexpr int S = K * K;
+  constexpr int U = SIHC_EV_UNROLL;  // tokens per lane per iteration
   const int BCG = blockDim.x, TL = blockDim.y;
   const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
   const int c0 = (slice * BCG + threadIdx.x) * V;
   if (c0 >= g.C) return;
   float bw[S][V], aw[S][V];
   load_weights<T, V, K>(beta, c0, bw);
-  const bool has_z = alpha != nullptr;
-  if (has_z) load_weights<T, V, K>(alpha, c0, aw);
+  if constexpr (HAS_Z) load_weights<T, V, K>(alpha, c0, aw);
   const int m_begin = chunk * tpb;
   const int m_end = min(m_begin + tpb, g.M);
-  for (int m = m_begin + threadIdx.y; m < m_end; m += TL) {
-    const int64_t p0 = cell_pixel0(m, g, index);
-    const int64_t zoff = int64_t(m) * g.C + c0;
-    float d[V];
-    load_vec<T, V>(dz + zoff, d);
-    float xv[S][V];
+  for (int m = m_begin + threadIdx.y; m < m_end; m += U * TL) {
+    int64_t p0[U], zoff[U];
+    bool ok[U];
+    float d[U][V];
+    float xv[U][S][V];
 #pragma unroll
-    for (int s = 0; s < S; ++s) load_vec<T, V>(x + slot_offset<K>(p0, s, g, c0), xv[s]);
-    float zacc[V];
+    for (int u = 0; u < U; ++u) {
+      ok[u] = m + u * TL < m_end;
+      const int mu = ok[u] ? m + u * TL : m;  // tail: reload a valid token, store nothing
+      p0[u] = cell_pixel0(mu, g, index);
+      zoff[u] = int64_t(mu) * g.C + c0;
+      load_vec<T, V>(dz + zoff[u], d[u]);
 #pragma unroll
-    for (int v = 0; v < V; ++v) zacc[v] = 0.f;
-#pragma unroll
-    for (int s = 0; s < S; ++s) {
-#pragma unroll
-      for (int v = 0; v < V; ++v) xv[s][v] = round_as<T>(fmaf(bw[s][v], d[v], xv[s][v]));
-      store_vec<T, V>(xo + slot_offset<K>(p0, s, g, c0), xv[s]);
-#pragma unroll
-      for (int v = 0; v < V; ++v) zacc[v] = fmaf(aw[s][v], xv[s][v], zacc[v]);
+      for (int s = 0; s < S; ++s) load_vec<T, V>(x + slot_offset<K>(p0[u], s, g, c0), xv[u][s]);
     }
-    if (has_z) store_vec<T, V>(zo + zoff, zacc);
+    load_fence();
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float zacc[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) zacc[v] = 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          xv[u][s][v] = round_as<T>(fmaf(bw[s][v], d[u][v], xv[u][s][v]));
+          if constexpr (HAS_Z) zacc[v] = fmaf(aw[s][v], xv[u][s][v], zacc[v]);
+        }
+      if (ok[u]) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) store_vec<T, V>(xo + slot_offset<K>(p0[u], s, g, c0), xv[u][s]);
+        if constexpr (HAS_Z) store_vec<T, V>(zo + zoff[u], zacc);
+      }
+    }
   }
 }
 
 // ----------------------------------------------------------------------------------
 // per-event fused backward (see sihc_event_backward in sihc_hip.h)
+//   HAS_H: grad_x_out given      HAS_G: read part (grad_z_out, x_out, alpha_next)
+//   HAS_W: write part (dz, beta)  STORE_T: store t as grad_x (else the caller aliases)
 // part[chunk][0][s][c] = partial grad_beta, part[chunk][1][s][c] = partial grad_alpha_next
 // ----------------------------------------------------------------------------------
-template <typename T, int V, int K>
-__global__ void __launch_bounds__(256) k_event_bwd(const T* __restrict__ gxo, const T* __restrict__ gzo,
+template <typename T, int V, int K, bool HAS_H, bool HAS_G, bool HAS_W, bool STORE_T>
+__global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_bwd(const T* __restrict__ gxo, const T* __restrict__ gzo,
                                                    const T* __restrict__ xo, const T* __restrict__ dz,
                                                    const T* __restrict__ beta,
                                                    const T* __restrict__ alpha, T* __restrict__ gx,
                                                    T* __restrict__ gdz, float* __restrict__ part,
                                                    const int32_t* __restrict__ index, Geo g, int tpb, int nslices) {
   constexpr int S = K * K;
+  constexpr int U = SIHC_EV_UNROLL;  // tokens per lane per iteration
   extern __shared__ float red[];
   const int BCG = blockDim.x, TL = blockDim.y;
   const int BC = BCG * V;
   const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
   const int c0 = slice * BC + threadIdx.x * V;
-  const bool active = c0 < g.C;
-  const bool has_h = gxo != nullptr;
-  const bool has_g = gzo != nullptr;   // read part: t += alpha*gz, grad_alpha partials
-  const bool has_w = beta != nullptr;  // write part: grad_dz, grad_beta partials
-  const bool store_t = gx != nullptr;  // else t == grad_x_out and the caller aliases it
-  float bw[S][V], aw[S][V];
   float db[S][V], da[S][V];
 #pragma unroll
   for (int s = 0; s < S; ++s)
@@ -467,64 +610,82 @@ __global__ void __launch_bounds__(256) k_event_bwd(const T* __restrict__ gxo, co
     for (int v = 0; v < V; ++v) {
       db[s][v] = 0.f;
       da[s][v] = 0.f;
-      aw[s][v] = 0.f;
-      bw[s][v] = 0.f;
     }
-  if (active) {
-    if (has_w) load_weights<T, V, K>(beta, c0, bw);
-    if (has_g) load_weights<T, V, K>(alpha, c0, aw);
+  if (c0 < g.C) {
+    float bw[S][V], aw[S][V];
+    if constexpr (HAS_W) load_weights<T, V, K>(beta, c0, bw);
+    if constexpr (HAS_G) load_weights<T, V, K>(alpha, c0, aw);
     const int m_begin = chunk * tpb;
     const int m_end = min(m_begin + tpb, g.M);
-    for (int m = m_begin + threadIdx.y; m < m_end; m += TL) {
-      const int64_t p0 = cell_pixel0(m, g, index);
-      const int64_t zoff = int64_t(m) * g.C + c0;
-      float gz[V], d[V];
+    for (int m = m_begin + threadIdx.y; m < m_end; m += U * TL) {
+      int64_t p0[U], zoff[U];
+      bool ok[U];
+      float gz[U][V], d[U][V], t[U][S][V], xv[U][S][V];
+      // ---- loads (tail tokens reload a valid token; their gz/d are zeroed below so
+      //      they add nothing to the weight gradients, and nothing is stored)
 #pragma unroll
-      for (int v = 0; v < V; ++v) {
-        gz[v] = 0.f;
-        d[v] = 0.f;
-      }
-      if (has_g) load_vec<T, V>(gzo + zoff, gz);
-      if (has_w) load_vec<T, V>(dz + zoff, d);
-      float gd[V];
+      for (int u = 0; u < U; ++u) {
+        ok[u] = m + u * TL < m_end;
+        const int mu = ok[u] ? m + u * TL : m;
+        p0[u] = cell_pixel0(mu, g, index);
+        zoff[u] = int64_t(mu) * g.C + c0;
+        if constexpr (HAS_G) load_vec<T, V>(gzo + zoff[u], gz[u]);
+        if constexpr (HAS_W) load_vec<T, V>(dz + zoff[u], d[u]);
 #pragma unroll
-      for (int v = 0; v < V; ++v) gd[v] = 0.f;
+        for (int s = 0; s < S; ++s) {
+          const int64_t off = slot_offset<K>(p0[u], s, g, c0);
+          if constexpr (HAS_H) {
+            load_vec<T, V>(gxo + off, t[u][s]);
+          } else {
 #pragma unroll
-      for (int s = 0; s < S; ++s) {
-        const int64_t off = slot_offset<K>(p0, s, g, c0);
-        float t[V];
-        if (has_h) {
-          load_vec<T, V>(gxo + off, t);
-        } else {
-#pragma unroll
-          for (int v = 0; v < V; ++v) t[v] = 0.f;
-        }
-        if (has_g) {
-          float xv[V];
-          load_vec<T, V>(xo + off, xv);
-#pragma unroll
-          for (int v = 0; v < V; ++v) {
-            da[s][v] = fmaf(xv[v], gz[v], da[s][v]);
-            t[v] = fmaf(aw[s][v], gz[v], t[v]);
+            for (int v = 0; v < V; ++v) t[u][s][v] = 0.f;
           }
-        }
-        if (store_t) store_vec<T, V>(gx + off, t);
-        if (has_w) {
-#pragma unroll
-          for (int v = 0; v < V; ++v) {
-            gd[v] = fmaf(bw[s][v], t[v], gd[v]);
-            db[s][v] = fmaf(d[v], t[v], db[s][v]);
-          }
+          if constexpr (HAS_G) load_vec<T, V>(xo + off, xv[u][s]);
         }
       }
-      if (has_w) store_vec<T, V>(gdz + zoff, gd);
+      load_fence();
+      // ---- compute and store
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (U > 1 && !ok[u]) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            gz[u][v] = 0.f;
+            d[u][v] = 0.f;
+          }
+        }
+        float gd[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) gd[v] = 0.f;
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            if constexpr (HAS_G) {
+              da[s][v] = fmaf(xv[u][s][v], gz[u][v], da[s][v]);
+              t[u][s][v] = fmaf(aw[s][v], gz[u][v], t[u][s][v]);
+            }
+            if constexpr (HAS_W) {
+              gd[v] = fmaf(bw[s][v], t[u][s][v], gd[v]);
+              db[s][v] = fmaf(d[u][v], t[u][s][v], db[s][v]);
+            }
+          }
+        if (ok[u]) {
+          if constexpr (STORE_T) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) store_vec<T, V>(gx + slot_offset<K>(p0[u], s, g, c0), t[u][s]);
+          }
+          if constexpr (HAS_W) store_vec<T, V>(gdz + zoff[u], gd);
+        }
+      }
     }
   }
-  // Block reduction of the two [S][V] accumulators; partial rows are [2][S][C].
+  // Block reduction of the [S][V] accumulators; partial rows are [2][S][C].
   float* prow = part + int64_t(chunk) * 2 * S * g.C;
   const int cs = slice * BC;
 #pragma unroll
   for (int w = 0; w < 2; ++w) {
+    if ((w == 0 && !HAS_W) || (w == 1 && !HAS_G)) continue;
     float flat[S * V];
 #pragma unroll
     for (int s = 0; s < S; ++s)
@@ -566,32 +727,14 @@ __global__ void __launch_bounds__(256) k_cells(const R* __restrict__ src, R* __r
   }
 }
 
-__global__ void __launch_bounds__(256) k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, int64_t n) {
+__global__ void __launch_bounds__(256) k_copy16(const u32x4* __restrict__ src, u32x4* __restrict__ dst, int64_t n) {
   const int64_t stride = int64_t(gridDim.x) * blockDim.x;
-  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) st(dst + i, ld(src + i));
 }
 
 __global__ void k_copy1(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t n) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) dst[i] = src[i];
-}
-
-// out0[c][s] = sum_k part[k][0][s][c]; out1[c][s] = sum_k part[k][1][s][c] (if out1).
-template <typename TO>
-__global__ void __launch_bounds__(256) k_finalize_pair(const float* __restrict__ part, TO* __restrict__ out0,
-                                                       TO* __restrict__ out1, int chunks, int S, int C) {
-  const int64_t n = int64_t(S) * C;
-  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= 2 * n) return;
-  const int w = int(i / n);
-  TO* out = w == 0 ? out0 : out1;
-  if (!out) return;
-  const int r = int(i - w * n);
-  const int s = r / C;
-  const int c = r - s * C;
-  float sum = 0.f;
-  for (int k = 0; k < chunks; ++k) sum += part[int64_t(k) * 2 * n + i];
-  out[int64_t(c) * S + s] = from_f32<TO>(sum);
 }
 
 // ==================================================================================
@@ -620,11 +763,11 @@ bool valid_dtype(int dtype) { return dtype == SIHC_DTYPE_F32 || dtype == SIHC_DT
 
 bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % uintptr_t(bytes)) == 0; }
 
-// Largest V in {8, 4, 1} (V*elem <= max_bytes) such that C % V == 0 and every pointer
-// is aligned to V*elem bytes. `elem` is the widest element size among the tensors.
-int pick_vec(int C, int elem, int max_bytes, const void* const* ptrs, int n) {
-  for (int v : {8, 4}) {
-    if (v * elem > max_bytes || C % v) continue;
+// Largest V in {8, 4, 2, 1} with V <= max_v and V*elem <= 16 such that C % V == 0 and
+// every pointer is aligned to V*elem bytes. `elem` is the widest element size.
+int pick_vec(int C, int elem, int max_v, const void* const* ptrs, int n) {
+  for (int v : {8, 4, 2}) {
+    if (v > max_v || v * elem > 16 || C % v) continue;
     bool ok = true;
     for (int i = 0; i < n && ok; ++i) ok = ptrs[i] == nullptr || aligned(ptrs[i], v * elem);
     if (ok) return v;
@@ -636,11 +779,11 @@ struct Shape2D {
   int bcg, tl, slices;
 };
 
-// Channel groups per block: 16 lanes of V channels (a 256-byte run per token row for
-// 16-byte vectors), reduced when the weight slice would not fit `lds_cap` bytes.
-Shape2D shape_for(int C, int V, int lds_per_channel, int lds_cap = 64 * 1024) {
+// Channel groups per block: `bcg0` lanes of V channels, fewer when C is small or the
+// weight slice would not fit `lds_cap` bytes.
+Shape2D shape_for(int C, int V, int bcg0, int lds_per_channel, int lds_cap = 64 * 1024) {
   const int CG = (C + V - 1) / V;
-  int bcg = 16;
+  int bcg = bcg0;
   while (bcg > 1 && bcg / 2 >= CG) bcg /= 2;
   while (bcg > 1 && int64_t(lds_per_channel) * bcg * V > lds_cap) bcg /= 2;
   Shape2D sh;
@@ -656,10 +799,10 @@ int chunk_count(int64_t M, int tokens_per_chunk, int max_chunks) {
   if (n > max_chunks) n = max_chunks;
   return int(n);
 }
-// Token chunks of the weight-gradient reductions: a function of sizes only, so that
-// the workspace size query and the launch agree.
-int wgrad_chunks(int64_t M) { return chunk_count(M, 512, 128); }
-int event_bwd_chunks(int64_t M) { return chunk_count(M, 256, 256); }
+// Token chunks of the reductions: functions of sizes only, so that the workspace
+// size queries and the launches agree.
+int wgrad_chunks(int64_t M) { return chunk_count(M, SIHC_WG_CHUNK, 128); }
+int event_bwd_chunks(int64_t M) { return chunk_count(M, SIHC_EV_CHUNK, 512); }
 
 int check_geometry(const char* what, int64_t batch, int grid, int cell, int channels, Geo* g) {
   if (batch < 0 || grid <= 0 || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
@@ -686,10 +829,11 @@ int check_events(const char* what, int events, const void* const* ptrs) {
   return SIHC_OK;
 }
 
+// Kernel-argument pointer pack; slots past n repeat the last pointer so that padded
+// event groups always load valid memory (their weights are zero or their sums unused).
 PtrPack pack(const void* const* ptrs, int n) {
   PtrPack p;
-  std::memset(&p, 0, sizeof(p));
-  for (int i = 0; i < n; ++i) p.p[i] = ptrs[i];
+  for (int i = 0; i < SIHC_MAX_EVENTS; ++i) p.p[i] = ptrs[i < n ? i : n - 1];
   return p;
 }
 
@@ -702,6 +846,7 @@ template <typename F>
 int with_vec(int v, F&& f) {
   if (v == 8) return f(IC<8>{});
   if (v == 4) return f(IC<4>{});
+  if (v == 2) return f(IC<2>{});
   return f(IC<1>{});
 }
 template <typename F>
@@ -709,10 +854,40 @@ int with_cell(int k, F&& f) {
   if (k == 2) return f(IC<2>{});
   return f(IC<4>{});
 }
+template <typename F>
+int with_bool(bool b, F&& f) {
+  if (b) return f(std::true_type{});
+  return f(std::false_type{});
+}
 
 // 1-D grid of slices x chunks (slices fastest: concurrently resident blocks cover whole
 // channel rows of a token range).
 unsigned blocks1d(int slices, int64_t chunks) { return unsigned(int64_t(slices) * chunks); }
+
+template <typename TO>
+int launch_fill_zero(void* out, int64_t n, hipStream_t st, const char* what) {
+  if (n <= 0) return SIHC_OK;
+  hipLaunchKernelGGL((k_fill_zero<TO>), dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, static_cast<TO*>(out), n);
+  return check_launch(what);
+}
+int fill_zero(int dtype, void* out, int64_t n, hipStream_t st, const char* what) {
+  return dtype == SIHC_DTYPE_F32 ? launch_fill_zero<float>(out, n, st, what)
+                                 : launch_fill_zero<bf16_t>(out, n, st, what);
+}
+
+int launch_finalize(const char* what, const float* part, void* out0, void* out1, int chunks, int R, int S, int C,
+                    bool pair, int zero_mask, int out_dtype, hipStream_t st) {
+  const int64_t n = int64_t(R) * S * C;
+  const unsigned blocks = unsigned((n + 31) / 32);
+  if (out_dtype == SIHC_DTYPE_F32) {
+    hipLaunchKernelGGL((k_finalize<float>), dim3(blocks), dim3(256), 0, st, part, static_cast<float*>(out0),
+                       static_cast<float*>(out1), chunks, R, S, C, pair ? 1 : 0, zero_mask);
+  } else {
+    hipLaunchKernelGGL((k_finalize<bf16_t>), dim3(blocks), dim3(256), 0, st, part, static_cast<bf16_t*>(out0),
+                       static_cast<bf16_t*>(out1), chunks, R, S, C, pair ? 1 : 0, zero_mask);
+  }
+  return check_launch(what);
+}
 
 int cells_copy(const char* what, bool gather, const void* src, const int32_t* index, void* dst, int64_t batch,
                int grid, int cell, int channels, int dtype, void* stream) {
@@ -746,9 +921,80 @@ int cells_copy(const char* what, bool gather, const void* src, const int32_t* in
     };
     return with_cell(cell, launch);
   };
-  if (row_bytes % 16 == 0 && aligned(src, 16) && aligned(dst, 16)) return go(uint4{});
+  if (row_bytes % 16 == 0 && aligned(src, 16) && aligned(dst, 16)) return go(u32x4{});
   if (row_bytes % 4 == 0 && aligned(src, 4) && aligned(dst, 4)) return go(uint32_t{});
   return go(uint16_t{});
+}
+
+// Shared launcher of the atomics-free weight-gradient reduction + finalize.
+int launch_wgrad(const char* what, const void* x, const void* const* z, void* out, int events, const Geo& g,
+                 int S, bool carrier, const int32_t* index, int dtype, int out_dtype, void* workspace,
+                 size_t workspace_bytes, hipStream_t st) {
+  const int chunks = wgrad_chunks(g.M);
+  const size_t need = size_t(chunks) * events * S * g.C * sizeof(float);
+  if (!workspace || workspace_bytes < need)
+    return fail(SIHC_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", what, need, workspace_bytes);
+  if (!aligned(workspace, 16)) return fail(SIHC_ERR_INVALID, "%s: workspace must be 16-byte aligned", what);
+  const int es = elem_size(dtype);
+  const void* ptrs[SIHC_MAX_EVENTS + 1];
+  for (int i = 0; i < events; ++i) ptrs[i] = z[i];
+  ptrs[events] = x;
+  const int emax = events <= 1 ? 1 : events <= 2 ? 2 : events <= 4 ? 4 : events <= 8 ? 8 : events <= 12 ? 12
+                   : events <= 16 ? 16 : events <= 24 ? 24 : 32;
+  // At most 64 fp32 accumulators per lane (the loaded z values need as many again).
+  const int V = pick_vec(g.C, es, std::max(1, 64 / emax), ptrs, events + 1);
+  const int CG = (g.C + V - 1) / V;
+  int bcg = 16;
+  while (bcg > 1 && bcg / 2 >= CG) bcg /= 2;
+  while (bcg * S > 256) bcg /= 2;
+  const int lanes = bcg * S;
+  const int tl = 256 / lanes;
+  const int slices = (CG + bcg - 1) / bcg;
+  const int tpb = int((int64_t(g.M) + chunks - 1) / chunks);
+  const size_t lds = size_t(tl) * lanes * V * sizeof(float);
+  const PtrPack pk = pack(z, events);
+  float* part = static_cast<float*>(workspace);
+  int rc = with_dtype(dtype, [&](auto t) {
+    using T = decltype(t);
+    return with_vec(V, [&](auto vv) {
+      constexpr int VV = decltype(vv)::value;
+      auto go = [&](auto em, auto kk, auto car) {
+        constexpr int EM = decltype(em)::value;
+        constexpr int KK = decltype(kk)::value;
+        constexpr bool CAR = decltype(car)::value;
+        if constexpr (EM * VV > 64 || VV * sizeof(T) > 16) {
+          return fail(SIHC_ERR_INVALID, "%s: internal accumulator width", what);
+        } else {
+          hipLaunchKernelGGL((k_wgrad<T, VV, KK, EM, CAR>), dim3(blocks1d(slices, chunks)), dim3(lanes, tl), lds, st,
+                             static_cast<const T*>(x), pk, part, index, events, bcg, g, tpb, slices);
+          return check_launch(what);
+        }
+      };
+      auto with_em = [&](auto kk, auto car) {
+        switch (emax) {
+          case 1: return go(IC<1>{}, kk, car);
+          case 2: return go(IC<2>{}, kk, car);
+          case 4: return go(IC<4>{}, kk, car);
+          case 8: return go(IC<8>{}, kk, car);
+          case 12: return go(IC<12>{}, kk, car);
+          case 16: return go(IC<16>{}, kk, car);
+          case 24: return go(IC<24>{}, kk, car);
+          default: return go(IC<32>{}, kk, car);
+        }
+      };
+      if (!carrier) return with_em(IC<2>{}, std::false_type{});
+      if (g.K == 2) return with_em(IC<2>{}, std::true_type{});
+      return with_em(IC<4>{}, std::true_type{});
+    });
+  });
+  if (rc) return rc;
+  return launch_finalize(what, part, out, nullptr, chunks, events, S, g.C, false, 0, out_dtype, st);
+}
+
+// Vector width of the per-event kernels: registers hold up to 2*S*V weights and 2*S*V
+// accumulators, so wide vectors are used only for the 4-slot cell.
+int event_vec(int C, int es, int cell, const void* const* ptrs, int n) {
+  return pick_vec(C, es, cell == 2 ? SIHC_EV_VEC : 2, ptrs, n);
 }
 
 }  // namespace
@@ -774,10 +1020,10 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
   const void* ptrs[SIHC_MAX_EVENTS + 1];
   for (int i = 0; i < events; ++i) ptrs[i] = out[i];
   ptrs[events] = x;
-  const int V = pick_vec(channels, es, 16, ptrs, events + 1);
+  const int V = pick_vec(channels, es, 8, ptrs, events + 1);
   const int S = cell * cell;
-  const Shape2D sh = shape_for(channels, V, events * S * 4);
-  const int tpb = sh.tl * 8;
+  const Shape2D sh = shape_for(channels, V, SIHC_RW_BCG, events * S * 4);
+  const int tpb = sh.tl * SIHC_RW_TPT;
   const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
   const size_t lds = size_t(events) * S * sh.bcg * V * 4;
   const PtrPack pk = pack(ptrs, events);
@@ -792,7 +1038,8 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
         return with_cell(cell, [&](auto kk) {
           constexpr int KK = decltype(kk)::value;
           hipLaunchKernelGGL((k_read<T, VV, KK>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), lds, st,
-                             static_cast<const T*>(x), static_cast<const T*>(alpha), pk, index, events, g, tpb, sh.slices);
+                             static_cast<const T*>(x), static_cast<const T*>(alpha), pk, index, events, g, tpb,
+                             sh.slices);
           return check_launch(what);
         });
       }
@@ -817,12 +1064,13 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
   ptrs[events] = add_x ? x : nullptr;
   ptrs[events + 1] = out;
   const int es = std::max(elem_size(x_dtype), elem_size(w_dtype));
-  const int V = pick_vec(channels, es, 16, ptrs, events + 2);
+  const int V = pick_vec(channels, es, 8, ptrs, events + 2);
   const int S = cell * cell;
-  const Shape2D sh = shape_for(channels, V, events * S * 4);
-  const int tpb = sh.tl * 8;
+  const int E4 = (events + 3) & ~3;
+  const Shape2D sh = shape_for(channels, V, SIHC_RW_BCG, E4 * S * 4);
+  const int tpb = sh.tl * SIHC_RW_TPT;
   const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
-  const size_t lds = size_t(events) * S * sh.bcg * V * 4;
+  const size_t lds = size_t(E4) * S * sh.bcg * V * 4;
   const PtrPack pk = pack(updates, events);
   hipStream_t st = static_cast<hipStream_t>(stream);
   auto launch = [&](auto tx, auto tw) {
@@ -835,10 +1083,13 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
       } else {
         return with_cell(cell, [&](auto kk) {
           constexpr int KK = decltype(kk)::value;
-          hipLaunchKernelGGL((k_write<TX, TW, VV, KK>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), lds,
-                             st, static_cast<const TX*>(x), pk, static_cast<const TW*>(beta), static_cast<TX*>(out),
-                             index, events, add_x ? 1 : 0, g, tpb, sh.slices);
-          return check_launch(what);
+          return with_bool(add_x != 0, [&](auto ax) {
+            constexpr bool AX = decltype(ax)::value;
+            hipLaunchKernelGGL((k_write<TX, TW, VV, KK, AX>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl),
+                               lds, st, static_cast<const TX*>(x), pk, static_cast<const TW*>(beta),
+                               static_cast<TX*>(out), index, events, g, tpb, sh.slices);
+            return check_launch(what);
+          });
         });
       }
     });
@@ -854,79 +1105,6 @@ size_t sihc_weight_grad_workspace_size(int events, int64_t batch, int grid, int 
   return size_t(wgrad_chunks(M)) * events * cell * cell * channels * sizeof(float);
 }
 
-namespace {
-// Shared launcher of the atomics-free weight-gradient reduction + finalize.
-int launch_wgrad(const char* what, const void* x, const void* const* z, void* out, int events, const Geo& g,
-                 int S, bool carrier, const int32_t* index, int dtype, int out_dtype, void* workspace,
-                 size_t workspace_bytes, hipStream_t st) {
-  const int chunks = wgrad_chunks(g.M);
-  const size_t need = size_t(chunks) * events * S * g.C * sizeof(float);
-  if (!workspace || workspace_bytes < need)
-    return fail(SIHC_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", what, need, workspace_bytes);
-  if (!aligned(workspace, 16)) return fail(SIHC_ERR_INVALID, "%s: workspace must be 16-byte aligned", what);
-  const int es = elem_size(dtype);
-  const void* ptrs[SIHC_MAX_EVENTS + 1];
-  for (int i = 0; i < events; ++i) ptrs[i] = z[i];
-  ptrs[events] = x;
-  const int emax = events <= 8 ? 8 : events <= 16 ? 16 : 32;
-  // Keep <= 128 fp32 accumulators per lane: 8 channels up to 16 events, else 4.
-  const int vmax_bytes = emax == 32 ? 4 * es : 16;
-  const int V = pick_vec(g.C, es, vmax_bytes, ptrs, events + 1);
-  const int CG = (g.C + V - 1) / V;
-  int bcg = 16;
-  while (bcg > 1 && bcg / 2 >= CG) bcg /= 2;
-  while (bcg * S > 256) bcg /= 2;
-  const int lanes = bcg * S;
-  const int tl = 256 / lanes;
-  const int slices = (CG + bcg - 1) / bcg;
-  const int tpb = int((int64_t(g.M) + chunks - 1) / chunks);
-  const size_t lds = size_t(tl) * lanes * V * sizeof(float);
-  const PtrPack pk = pack(z, events);
-  float* part = static_cast<float*>(workspace);
-  int rc = with_dtype(dtype, [&](auto t) {
-    using T = decltype(t);
-    return with_vec(V, [&](auto vv) {
-      constexpr int VV = decltype(vv)::value;
-      if constexpr (VV * sizeof(T) > 16) {
-        return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
-      } else {
-        auto go = [&](auto em, auto kk, auto car) {
-          constexpr int EM = decltype(em)::value;
-          constexpr int KK = decltype(kk)::value;
-          constexpr bool CAR = decltype(car)::value != 0;
-          if constexpr (EM * VV > 128) {
-            return fail(SIHC_ERR_INVALID, "%s: internal accumulator width", what);
-          } else {
-            hipLaunchKernelGGL((k_wgrad<T, VV, KK, EM, CAR>), dim3(blocks1d(slices, chunks)), dim3(lanes, tl), lds, st,
-                               static_cast<const T*>(x), pk, part, index, events, bcg, g, tpb, slices);
-            return check_launch(what);
-          }
-        };
-        auto with_em = [&](auto kk, auto car) {
-          if (emax == 8) return go(IC<8>{}, kk, car);
-          if (emax == 16) return go(IC<16>{}, kk, car);
-          return go(IC<32>{}, kk, car);
-        };
-        if (!carrier) return with_em(IC<2>{}, IC<0>{});
-        if (g.K == 2) return with_em(IC<2>{}, IC<1>{});
-        return with_em(IC<4>{}, IC<1>{});
-      }
-    });
-  });
-  if (rc) return rc;
-  const int64_t n = int64_t(events) * S * g.C;
-  const unsigned blocks = unsigned((n + 255) / 256);
-  if (out_dtype == SIHC_DTYPE_F32) {
-    hipLaunchKernelGGL((k_finalize<float>), dim3(blocks), dim3(256), 0, st, part, static_cast<float*>(out), chunks,
-                       events, S, g.C);
-  } else {
-    hipLaunchKernelGGL((k_finalize<bf16_t>), dim3(blocks), dim3(256), 0, st, part, static_cast<bf16_t*>(out),
-                       chunks, events, S, g.C);
-  }
-  return check_launch(what);
-}
-}  // namespace
-
 int sihc_weight_grad(const void* x, const void* const* z, void* out, int events, int64_t batch, int grid, int cell,
                      int channels, const int32_t* index, int dtype, int out_dtype, void* workspace,
                      size_t workspace_bytes, void* stream) {
@@ -936,14 +1114,11 @@ int sihc_weight_grad(const void* x, const void* const* z, void* out, int events,
   if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
   if (!x || !out) return fail(SIHC_ERR_INVALID, "%s: null input", what);
   if (int rc = check_events(what, events, z)) return rc;
-  if (g.M == 0) {
-    // Empty reduction: zero gradient.
-    hipError_t e = hipMemsetAsync(out, 0, size_t(events) * cell * cell * channels * elem_size(out_dtype),
-                                  static_cast<hipStream_t>(stream));
-    return e == hipSuccess ? SIHC_OK : fail(SIHC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
-  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (g.M == 0)  // empty reduction: zero gradient
+    return fill_zero(out_dtype, out, int64_t(events) * cell * cell * channels, st, what);
   return launch_wgrad(what, x, z, out, events, g, cell * cell, true, index, dtype, out_dtype, workspace,
-                      workspace_bytes, static_cast<hipStream_t>(stream));
+                      workspace_bytes, st);
 }
 
 int sihc_triangular(const void* base, const void* const* updates, const void* gamma, void* out, int active,
@@ -959,11 +1134,12 @@ int sihc_triangular(const void* base, const void* const* updates, const void* ga
   for (int i = 0; i < active; ++i) ptrs[i] = updates[i];
   ptrs[active] = base;
   ptrs[active + 1] = out;
-  const int V = pick_vec(channels, es, 16, ptrs, active + 2);
-  const Shape2D sh = shape_for(channels, V, active * 4);
-  const int tpb = sh.tl * 8;
+  const int V = pick_vec(channels, es, 8, ptrs, active + 2);
+  const int A4 = (active + 3) & ~3;
+  const Shape2D sh = shape_for(channels, V, SIHC_RW_BCG, A4 * 4);
+  const int tpb = sh.tl * SIHC_RW_TPT;
   const int64_t chunks = (rows + tpb - 1) / tpb;
-  const size_t lds = size_t(active) * sh.bcg * V * 4;
+  const size_t lds = size_t(A4) * sh.bcg * V * 4;
   const PtrPack pk = pack(updates, active);
   hipStream_t st = static_cast<hipStream_t>(stream);
   return with_dtype(dtype, [&](auto t) {
@@ -998,11 +1174,8 @@ int sihc_triangular_gamma_grad(const void* grad, const void* const* updates, voi
   if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
   if (!grad || !out) return fail(SIHC_ERR_INVALID, "%s: null input", what);
   if (int rc = check_events(what, active, updates)) return rc;
-  if (rows == 0) {
-    hipError_t e = hipMemsetAsync(out, 0, size_t(active) * channels * elem_size(out_dtype),
-                                  static_cast<hipStream_t>(stream));
-    return e == hipSuccess ? SIHC_OK : fail(SIHC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
-  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (rows == 0) return fill_zero(out_dtype, out, int64_t(active) * channels, st, what);
   Geo g;
   g.M = int(rows);
   g.GG = 1;
@@ -1011,16 +1184,8 @@ int sihc_triangular_gamma_grad(const void* grad, const void* const* updates, voi
   g.GK = 1;
   g.C = channels;
   return launch_wgrad(what, grad, updates, out, active, g, 1, false, nullptr, dtype, out_dtype, workspace,
-                      workspace_bytes, static_cast<hipStream_t>(stream));
+                      workspace_bytes, st);
 }
-
-namespace {
-// Vector width of the per-event kernels: registers hold 2*S*V weights (and, backward,
-// 2*S*V accumulators), so wide vectors are used only for the 4-slot cell.
-int event_vec(int C, int es, int cell, const void* const* ptrs, int n) {
-  return pick_vec(C, es, cell == 2 ? 16 : 2 * es, ptrs, n);
-}
-}  // namespace
 
 int sihc_event_forward(const void* x, const void* dz, const void* beta, const void* alpha_next, void* x_out,
                        void* z_out, int64_t batch, int grid, int cell, int channels, const int32_t* index, int dtype,
@@ -1035,36 +1200,37 @@ int sihc_event_forward(const void* x, const void* dz, const void* beta, const vo
   if (g.M == 0) return SIHC_OK;
   const int es = elem_size(dtype);
   const int S = cell * cell;
-  const void* ptrs[] = {x, dz, x_out, z_out};
   if (!aligned(beta, std::min(16, S * es)) || (alpha_next && !aligned(alpha_next, std::min(16, S * es))))
     return fail(SIHC_ERR_INVALID, "%s: weights must be aligned to %d bytes", what, std::min(16, S * es));
+  const void* ptrs[] = {x, dz, x_out, z_out};
   int V = event_vec(channels, es, cell, ptrs, 4);
-  // Weight rows are loaded as V*S contiguous elements: need V*S*es alignment.
-  while (V > 1 && (!aligned(beta, V * S * es) || (alpha_next && !aligned(alpha_next, V * S * es)))) V = V == 8 ? 4 : 1;
-  const Shape2D sh = shape_for(channels, V, 0);
-  const int tpb = sh.tl * 8;
+  // Weight rows are loaded as V*S contiguous elements: need min(16, V*S*es) alignment.
+  while (V > 1 && (!aligned(beta, std::min(16, V * S * es)) ||
+                   (alpha_next && !aligned(alpha_next, std::min(16, V * S * es)))))
+    V /= 2;
+  const Shape2D sh = shape_for(channels, V, SIHC_EV_BCG, 0);
+  const int tpb = sh.tl * SIHC_EV_TPT;
   const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
   hipStream_t st = static_cast<hipStream_t>(stream);
   return with_dtype(dtype, [&](auto t) {
     using T = decltype(t);
     return with_vec(V, [&](auto vv) {
       constexpr int VV = decltype(vv)::value;
-      if constexpr (VV * sizeof(T) > 16) {
-        return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
-      } else {
-        return with_cell(cell, [&](auto kk) {
-          constexpr int KK = decltype(kk)::value;
-          if constexpr (KK == 4 && VV > 2) {
-            return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
-          } else {
-            hipLaunchKernelGGL((k_event_fwd<T, VV, KK>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), 0, st,
-                               static_cast<const T*>(x), static_cast<const T*>(dz), static_cast<const T*>(beta),
+      return with_cell(cell, [&](auto kk) {
+        constexpr int KK = decltype(kk)::value;
+        if constexpr (VV * sizeof(T) > 16 || (KK == 4 && VV > 2) || VV > SIHC_EV_VEC) {
+          return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
+        } else {
+          return with_bool(alpha_next != nullptr, [&](auto hz) {
+            constexpr bool HZ = decltype(hz)::value;
+            hipLaunchKernelGGL((k_event_fwd<T, VV, KK, HZ>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), 0,
+                               st, static_cast<const T*>(x), static_cast<const T*>(dz), static_cast<const T*>(beta),
                                static_cast<const T*>(alpha_next), static_cast<T*>(x_out), static_cast<T*>(z_out),
                                index, g, tpb, sh.slices);
             return check_launch(what);
-          }
-        });
-      }
+          });
+        }
+      });
     });
   });
 }
@@ -1085,20 +1251,23 @@ int sihc_event_backward(const void* grad_x_out, const void* grad_z_out, const vo
   if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
   if (!valid_dtype(dtype) || !valid_dtype(w_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
   const bool has_w = beta != nullptr;
+  const bool has_g = grad_z_out != nullptr;
+  const bool has_h = grad_x_out != nullptr;
   if (has_w != (dz != nullptr) || has_w != (grad_dz != nullptr) || has_w != (grad_beta != nullptr))
     return fail(SIHC_ERR_INVALID, "%s: beta, dz, grad_dz and grad_beta must all be given or all be NULL", what);
-  if (grad_z_out && (!alpha_next || !x_out || !grad_alpha_next))
+  if (has_g && (!alpha_next || !x_out || !grad_alpha_next))
     return fail(SIHC_ERR_INVALID, "%s: grad_z_out needs alpha_next, x_out and grad_alpha_next", what);
-  if (!has_w && !grad_z_out) return fail(SIHC_ERR_INVALID, "%s: neither a write nor a read part", what);
-  if (!grad_x && grad_z_out)
+  if (!has_w && !has_g) return fail(SIHC_ERR_INVALID, "%s: neither a write nor a read part", what);
+  if (!grad_x && has_g)
     return fail(SIHC_ERR_INVALID, "%s: grad_x may be NULL only without grad_z_out (it equals grad_x_out)", what);
   const int S = cell * cell;
+  const int64_t wn = int64_t(S) * channels;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (g.M == 0) {
-    hipError_t e = has_w ? hipMemsetAsync(grad_beta, 0, size_t(S) * channels * elem_size(w_dtype), st) : hipSuccess;
-    if (e == hipSuccess && grad_alpha_next)
-      e = hipMemsetAsync(grad_alpha_next, 0, size_t(S) * channels * elem_size(w_dtype), st);
-    return e == hipSuccess ? SIHC_OK : fail(SIHC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    if (has_w)
+      if (int rc = fill_zero(w_dtype, grad_beta, wn, st, what)) return rc;
+    if (grad_alpha_next) return fill_zero(w_dtype, grad_alpha_next, wn, st, what);
+    return SIHC_OK;
   }
   const int chunks = event_bwd_chunks(g.M);
   const size_t need = size_t(chunks) * 2 * S * channels * sizeof(float);
@@ -1106,56 +1275,57 @@ int sihc_event_backward(const void* grad_x_out, const void* grad_z_out, const vo
     return fail(SIHC_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", what, need, workspace_bytes);
   if (!aligned(workspace, 16)) return fail(SIHC_ERR_INVALID, "%s: workspace must be 16-byte aligned", what);
   const int es = elem_size(dtype);
-  const void* ptrs[] = {grad_x_out, grad_z_out, x_out, dz, grad_x, grad_dz};
   if ((beta && !aligned(beta, std::min(16, S * es))) || (alpha_next && !aligned(alpha_next, std::min(16, S * es))))
     return fail(SIHC_ERR_INVALID, "%s: weights must be aligned to %d bytes", what, std::min(16, S * es));
+  const void* ptrs[] = {grad_x_out, grad_z_out, x_out, dz, grad_x, grad_dz};
   int V = event_vec(channels, es, cell, ptrs, 6);
-  while (V > 1 && (!aligned(beta, V * S * es) || (grad_z_out && !aligned(alpha_next, V * S * es)))) V = V == 8 ? 4 : 1;
-  const Shape2D sh = shape_for(channels, V, 0);
+  while (V > 1 && ((beta && !aligned(beta, std::min(16, V * S * es))) ||
+                   (has_g && !aligned(alpha_next, std::min(16, V * S * es)))))
+    V /= 2;
+  const Shape2D sh = shape_for(channels, V, SIHC_EV_BCG, 0);
   const int tpb = int((int64_t(g.M) + chunks - 1) / chunks);
   const size_t lds = size_t(sh.tl) * sh.bcg * S * V * sizeof(float);  // TL x (BCG*S*V) floats
   float* part = static_cast<float*>(workspace);
+  const bool store_t = grad_x != nullptr;
+  // Valid part combinations: read part present (t stored), or write part only.
+  const int mode = has_g ? (has_w ? 0 : 1) : (store_t ? 2 : 3);
   int rc = with_dtype(dtype, [&](auto t) {
     using T = decltype(t);
     return with_vec(V, [&](auto vv) {
       constexpr int VV = decltype(vv)::value;
-      if constexpr (VV * sizeof(T) > 16) {
-        return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
-      } else {
-        return with_cell(cell, [&](auto kk) {
-          constexpr int KK = decltype(kk)::value;
-          if constexpr (KK == 4 && VV > 2) {
-            return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
-          } else {
-            hipLaunchKernelGGL((k_event_bwd<T, VV, KK>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), lds, st,
-                               static_cast<const T*>(grad_x_out), static_cast<const T*>(grad_z_out),
-                               static_cast<const T*>(x_out), static_cast<const T*>(dz), static_cast<const T*>(beta),
-                               static_cast<const T*>(alpha_next), static_cast<T*>(grad_x), static_cast<T*>(grad_dz),
-                               part, index, g, tpb, sh.slices);
-            return check_launch(what);
-          }
-        });
-      }
+      return with_cell(cell, [&](auto kk) {
+        constexpr int KK = decltype(kk)::value;
+        if constexpr (VV * sizeof(T) > 16 || (KK == 4 && VV > 2) || VV > SIHC_EV_VEC) {
+          return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
+        } else {
+          return with_bool(has_h, [&](auto hh) {
+            constexpr bool HH = decltype(hh)::value;
+            auto go = [&](auto hg, auto hw, auto stt) {
+              constexpr bool HG = decltype(hg)::value, HW = decltype(hw)::value, STT = decltype(stt)::value;
+              hipLaunchKernelGGL((k_event_bwd<T, VV, KK, HH, HG, HW, STT>), dim3(blocks1d(sh.slices, chunks)),
+                                 dim3(sh.bcg, sh.tl), lds, st, static_cast<const T*>(grad_x_out),
+                                 static_cast<const T*>(grad_z_out), static_cast<const T*>(x_out),
+                                 static_cast<const T*>(dz), static_cast<const T*>(beta),
+                                 static_cast<const T*>(alpha_next), static_cast<T*>(grad_x), static_cast<T*>(grad_dz),
+                                 part, index, g, tpb, sh.slices);
+              return check_launch(what);
+            };
+            switch (mode) {
+              case 0: return go(std::true_type{}, std::true_type{}, std::true_type{});
+              case 1: return go(std::true_type{}, std::false_type{}, std::true_type{});
+              case 2: return go(std::false_type{}, std::true_type{}, std::true_type{});
+              default: return go(std::false_type{}, std::true_type{}, std::false_type{});
+            }
+          });
+        }
+      });
     });
   });
   if (rc) return rc;
-  // Partial rows are [chunks][2][S][C]: row 0 -> grad_beta, row 1 -> grad_alpha_next.
-  const int64_t n = int64_t(S) * channels;
-  const unsigned blocks = unsigned((2 * n + 255) / 256);
-  void* gan = grad_z_out ? grad_alpha_next : nullptr;
-  if (w_dtype == SIHC_DTYPE_F32) {
-    hipLaunchKernelGGL((k_finalize_pair<float>), dim3(blocks), dim3(256), 0, st, part, static_cast<float*>(grad_beta),
-                       static_cast<float*>(gan), chunks, S, channels);
-  } else {
-    hipLaunchKernelGGL((k_finalize_pair<bf16_t>), dim3(blocks), dim3(256), 0, st, part,
-                       static_cast<bf16_t*>(grad_beta), static_cast<bf16_t*>(gan), chunks, S, channels);
-  }
-  if (int rc2 = check_launch(what)) return rc2;
-  if (grad_alpha_next && !grad_z_out) {
-    hipError_t e = hipMemsetAsync(grad_alpha_next, 0, size_t(n) * elem_size(w_dtype), st);
-    if (e != hipSuccess) return fail(SIHC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
-  }
-  return SIHC_OK;
+  // Partial rows are [chunks][2][S][C]: row 0 -> grad_beta, row 1 -> grad_alpha_next
+  // (written as zeros when there is no read part).
+  return launch_finalize(what, part, has_w ? grad_beta : nullptr, grad_alpha_next, chunks, 2, S, channels, true,
+                         has_g ? 0 : 2, w_dtype, st);
 }
 
 int sihc_gather_cells(const void* x, const int32_t* index, void* cells, int64_t batch, int grid, int cell,
@@ -1177,8 +1347,8 @@ int sihc_copy(const void* src, void* dst, size_t bytes, void* stream) {
     const int64_t n = int64_t(bytes / 16);
     int64_t blocks = (n + 255) / 256;
     if (blocks > 256 * 64) blocks = 256 * 64;
-    hipLaunchKernelGGL(k_copy16, dim3(unsigned(blocks)), dim3(256), 0, st, static_cast<const uint4*>(src),
-                       static_cast<uint4*>(dst), n);
+    hipLaunchKernelGGL(k_copy16, dim3(unsigned(blocks)), dim3(256), 0, st, static_cast<const u32x4*>(src),
+                       static_cast<u32x4*>(dst), n);
   } else {
     const int64_t n = int64_t(bytes);
     hipLaunchKernelGGL(k_copy1, dim3(unsigned((n + 255) / 256)), dim3(256), 0, st, static_cast<const uint8_t*>(src),

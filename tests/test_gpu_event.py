@@ -96,7 +96,7 @@ def test_event_op_handles_unused_outputs():
     beta = torch.randn(32, 4, device="cuda", requires_grad=True)
     alpha = torch.randn(32, 4, device="cuda", requires_grad=True)
     x_out, z_out = event_write_read(x, dz, beta, alpha)
-    gx, gdz, gb, ga = torch.autograd.grad(z_out.sum(), (x, dz, beta, alpha))
+    gx, gdz, gb, ga = torch.autograd.grad(z_out.sum(), (x, dz, beta, alpha), retain_graph=True)
     ref = O.event_backward(None, torch.ones(2, 16, 32), x_out.detach().cpu(), dz.detach().cpu(),
                            beta.detach().cpu(), alpha.detach().cpu())
     for a, b in zip((gx, gdz, gb, ga), ref):
