@@ -50,9 +50,10 @@ def parse_args():
     p.add_argument("--seed", type=int, default=2)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
-    p.add_argument("--mode", choices=("step", "calibrate"), default="step",
+    p.add_argument("--mode", choices=("step", "calibrate", "kernels"), default="step",
                    help="step: the benchmark (default); calibrate: a 1 GiB copy-kernel launch plus single "
-                        "event forward/backward launches at the same shape, for HBM counter runs")
+                        "event forward/backward launches at the same shape, for HBM counter runs; kernels: "
+                        "every HIP kernel timed alone at the benchmark shape (one JSON line per kernel)")
     return p.parse_args()
 
 
@@ -253,6 +254,68 @@ def calibrate(args) -> None:
                       "event_backward_read": 10 * U, "event_backward_written": 5 * U}), flush=True)
 
 
+def kernels(args) -> None:
+    """Each library kernel alone at the SiHC-XL shape (batch 256, D=1152, bf16), including
+    the stage-API ops the reference's sublayer.py calls (events 16/24, active prefixes up to
+    23) and the config-3 gather/scatter (batch 128). GB/s = algorithmic bytes / mean time."""
+    import torch
+
+    from sihc_hip import launch
+    from sihc_hip.indexed import group_index
+
+    dev = torch.device("cuda", 0)
+    bf = torch.bfloat16
+    B, C, S = args.batch, args.channels, 4
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    r = lambda shape, m=0.0, sd=1.0: (m + sd * torch.randn(shape, device=dev, generator=g)).to(bf)  # noqa: E731
+    x = r((B, 32, 32, C))
+    ws = [r((B, 256, C)) for _ in range(25)]
+    alpha = r((24, C, S), 0.25, 0.02)
+    beta = r((24, C, S), 1.0, 0.02)
+    gamma = (0.05 * torch.randn(24, C, device=dev, generator=g))
+    U = B * 256 * C * ELEM
+
+    def timed(fn, iters=10):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / iters * 1e-3
+
+    cases = []
+    for e in (1, 16, 24):
+        cases.append((f"read E={e}", (S + e) * U, lambda e=e: launch.read(x, alpha[:e])))
+    for e in (1, 16, 24):
+        cases.append((f"write E={e}", (2 * S + e) * U, lambda e=e: launch.write(x, ws[:e], beta[:e])))
+    cases.append(("write_impl (add_x=False) E=24", (S + 24) * U, lambda: launch.write(x, ws[:24], alpha, add_x=False)))
+    for e in (16, 24):
+        cases.append((f"weight_grad E={e}", (S + e) * U, lambda e=e: launch.weight_grad(x, ws[:e], beta[:e])))
+    for a in (1, 12, 23):
+        cases.append((f"triangular A={a}", (a + 2) * U, lambda a=a: launch.triangular(ws[24], ws[:a], gamma[:a])))
+    for a in (12, 23):
+        cases.append((f"triangular_gamma_grad A={a}", (a + 1) * U,
+                      lambda a=a: launch.triangular_gamma_grad(ws[24], ws[:a], gamma[:a])))
+    cases.append(("event_forward", 10 * U, lambda: launch.event_forward(x, ws[0], beta[0], alpha[1])))
+    h = r((B, 32, 32, C), 0.0, 1e-2)
+    cases.append(("event_backward", 15 * U,
+                  lambda: launch.event_backward(h, ws[1], x, ws[0], beta[0], alpha[1])))
+    xb = x[: B // 2].contiguous()
+    idx = group_index(B // 2, 16, 5, seed=3).to(dev)
+    cells = launch.gather_cells(xb, idx, S)
+    cases.append(("gather_cells (config 3)", 2 * S * U // 2, lambda: launch.gather_cells(xb, idx, S)))
+    cases.append(("scatter_cells (config 3)", 2 * S * U // 2, lambda: launch.scatter_cells(cells, idx)))
+    for name, nbytes, fn in cases:
+        t = timed(fn)
+        print(json.dumps({"kernel": name, "us": round(t * 1e6, 1), "bytes": nbytes,
+                          "GB/s": round(nbytes / t / 1e9, 1), "frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}),
+              flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -267,6 +330,9 @@ def main():
     torch.cuda.set_device(0)
     if args.mode == "calibrate":
         calibrate(args)
+        return
+    if args.mode == "kernels":
+        kernels(args)
         return
     print(f"[bench] building step: batch={args.batch} C={args.channels} events={args.events}", file=sys.stderr,
           flush=True)

@@ -54,6 +54,9 @@
 #ifndef SIHC_RW_BCG  // channel-group lanes per block, read / write / triangular
 #define SIHC_RW_BCG 16
 #endif
+#ifndef SIHC_RW_UNROLL  // tokens per lane per loop iteration, read / write / triangular
+#define SIHC_RW_UNROLL 2
+#endif
 #ifndef SIHC_RW_TPT  // tokens per lane, read / write / triangular
 #define SIHC_RW_TPT 8
 #endif
@@ -220,20 +223,36 @@ __device__ __forceinline__ int64_t slot_offset(int64_t pix0, int s, const Geo& g
   return (pix0 + int64_t(s / K) * g.GK + (s % K)) * g.C + c;
 }
 
-// Stage a [E, C, S] weight stack's channel slice [cs, cs+BC) into LDS as [Epad][S][BC]
-// fp32, zero-filling padded events (e >= E) and channels past C.
-template <typename TW>
-__device__ __forceinline__ void stage_weights(float* lds, const TW* __restrict__ w, int E, int Epad, int S, int BC,
+// LDS layout of a staged weight slice: row r = e*S + s, channel cl = cg*V + v of the
+// block's slice. For V >= 4 the row is stored as [V/4][BCG][4] so that the BCG lanes of
+// a wave read 16 consecutive bytes each from consecutive addresses (one conflict-free
+// ds_read_b128 per 4 channels); narrower vectors use the plain [BCG*V] row.
+template <int V>
+__device__ __forceinline__ int lds_w(int row, int cg, int v, int BCG) {
+  if constexpr (V >= 4) {
+    return ((row * (V / 4) + v / 4) * BCG + cg) * 4 + (v & 3);
+  } else {
+    return row * BCG * V + cg * V + v;
+  }
+}
+
+// Stage a [E, C, S] weight stack's channel slice [cs, cs+BCG*V) into LDS (layout of
+// lds_w, rows e*S+s for e < Epad), zero-filling padded events (e >= E) and channels
+// past C.
+template <int V, typename TW>
+__device__ __forceinline__ void stage_weights(float* lds, const TW* __restrict__ w, int E, int Epad, int S, int BCG,
                                               int cs, int C) {
+  const int BC = BCG * V;
   const int tid = threadIdx.y * blockDim.x + threadIdx.x;
   const int nthr = blockDim.x * blockDim.y;
-  for (int i = tid; i < Epad * BC * S; i += nthr) {  // global [e][c][s] -> LDS [e][s][c]
+  for (int i = tid; i < Epad * BC * S; i += nthr) {  // global [e][c][s], read coalesced
     const int e = i / (BC * S);
     const int r = i - e * BC * S;
     const int cl = r / S;
     const int s = r - cl * S;
     const int c = cs + cl;
-    lds[(e * S + s) * BC + cl] = (e < E && c < C) ? to_f32(w[(int64_t(e) * C + c) * S + s]) : 0.f;
+    const int cg = cl / V;
+    lds[lds_w<V>(e * S + s, cg, cl - cg * V, BCG)] = (e < E && c < C) ? to_f32(w[(int64_t(e) * C + c) * S + s]) : 0.f;
   }
   __syncthreads();
 }
@@ -247,34 +266,49 @@ __global__ void __launch_bounds__(256) k_read(const T* __restrict__ x, const T* 
                                               PtrPack out, const int32_t* __restrict__ index,
                                               int E, Geo g, int tpb, int nslices) {
   constexpr int S = K * K;
+  constexpr int U = SIHC_RW_UNROLL;  // tokens per lane per iteration: each LDS weight feeds U tokens
   extern __shared__ float lds[];
   const int BCG = blockDim.x, TL = blockDim.y;
   const int BC = BCG * V;
   const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
   const int cs = slice * BC;
-  stage_weights(lds, alpha, E, E, S, BC, cs, g.C);
-  const int cl0 = threadIdx.x * V;
-  const int c0 = cs + cl0;
+  stage_weights<V>(lds, alpha, E, E, S, BCG, cs, g.C);
+  const int c0 = cs + threadIdx.x * V;
   if (c0 >= g.C) return;
   const int m_begin = chunk * tpb;
   const int m_end = min(m_begin + tpb, g.M);
-  for (int m = m_begin + threadIdx.y; m < m_end; m += TL) {
-    const int64_t p0 = cell_pixel0(m, g, index);
-    float xv[S][V];
+  for (int m = m_begin + threadIdx.y; m < m_end; m += U * TL) {
+    bool ok[U];
+    int64_t zoff[U];
+    float xv[U][S][V];
 #pragma unroll
-    for (int s = 0; s < S; ++s) load_vec<T, V>(x + slot_offset<K>(p0, s, g, c0), xv[s]);
+    for (int u = 0; u < U; ++u) {
+      ok[u] = m + u * TL < m_end;
+      const int mu = ok[u] ? m + u * TL : m;  // tail: reload a valid token, store nothing
+      const int64_t p0 = cell_pixel0(mu, g, index);
+      zoff[u] = int64_t(mu) * g.C + c0;
+#pragma unroll
+      for (int s = 0; s < S; ++s) load_vec<T, V>(x + slot_offset<K>(p0, s, g, c0), xv[u][s]);
+    }
     load_fence();
-    const int64_t zoff = int64_t(m) * g.C + c0;
     for (int e = 0; e < E; ++e) {
-      const float* a = lds + e * S * BC + cl0;
-      float acc[V];
+      float acc[U][V];
 #pragma unroll
-      for (int v = 0; v < V; ++v) acc[v] = 0.f;
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int v = 0; v < V; ++v) acc[u][v] = 0.f;
 #pragma unroll
       for (int s = 0; s < S; ++s)
 #pragma unroll
-        for (int v = 0; v < V; ++v) acc[v] = fmaf(a[s * BC + v], xv[s][v], acc[v]);
-      store_vec<T, V>(static_cast<T*>(const_cast<void*>(out.p[e])) + zoff, acc);
+        for (int v = 0; v < V; ++v) {
+          const float a = lds[lds_w<V>(e * S + s, threadIdx.x, v, BCG)];
+#pragma unroll
+          for (int u = 0; u < U; ++u) acc[u][v] = fmaf(a, xv[u][s][v], acc[u][v]);
+        }
+      T* dst = static_cast<T*>(const_cast<void*>(out.p[e]));
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (ok[u]) store_vec<T, V>(dst + zoff[u], acc[u]);
     }
   }
 }
@@ -290,47 +324,63 @@ __global__ void __launch_bounds__(256) k_write(const TX* __restrict__ x, PtrPack
                                                const int32_t* __restrict__ index, int E, Geo g, int tpb,
                                                int nslices) {
   constexpr int S = K * K;
+  constexpr int U = SIHC_RW_UNROLL;  // tokens per lane per iteration: each LDS weight feeds U tokens
+  constexpr int EG = U > 1 ? 2 : 4;  // events per load group
   extern __shared__ float lds[];
   const int BCG = blockDim.x, TL = blockDim.y;
   const int BC = BCG * V;
   const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
   const int cs = slice * BC;
   const int E4 = (E + 3) & ~3;
-  stage_weights(lds, beta, E, E4, S, BC, cs, g.C);
-  const int cl0 = threadIdx.x * V;
-  const int c0 = cs + cl0;
+  stage_weights<V>(lds, beta, E, E4, S, BCG, cs, g.C);
+  const int c0 = cs + threadIdx.x * V;
   if (c0 >= g.C) return;
   const int m_begin = chunk * tpb;
   const int m_end = min(m_begin + tpb, g.M);
-  for (int m = m_begin + threadIdx.y; m < m_end; m += TL) {
-    const int64_t p0 = cell_pixel0(m, g, index);
-    const int64_t zoff = int64_t(m) * g.C + c0;
-    float acc[S][V];
-    if constexpr (ADD_X) {
+  for (int m = m_begin + threadIdx.y; m < m_end; m += U * TL) {
+    bool ok[U];
+    int64_t p0[U], zoff[U];
+    float acc[U][S][V];
 #pragma unroll
-      for (int s = 0; s < S; ++s) load_vec<TX, V>(x + slot_offset<K>(p0, s, g, c0), acc[s]);
-    } else {
+    for (int u = 0; u < U; ++u) {
+      ok[u] = m + u * TL < m_end;
+      const int mu = ok[u] ? m + u * TL : m;  // tail: reload a valid token, store nothing
+      p0[u] = cell_pixel0(mu, g, index);
+      zoff[u] = int64_t(mu) * g.C + c0;
+      if constexpr (ADD_X) {
 #pragma unroll
-      for (int s = 0; s < S; ++s)
-#pragma unroll
-        for (int v = 0; v < V; ++v) acc[s][v] = 0.f;
-    }
-    for (int e = 0; e < E4; e += 4) {
-      float dz[4][V];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) load_vec<TW, V>(static_cast<const TW*>(upd.p[e + q]) + zoff, dz[q]);
-      load_fence();
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float* b = lds + (e + q) * S * BC + cl0;
+        for (int s = 0; s < S; ++s) load_vec<TX, V>(x + slot_offset<K>(p0[u], s, g, c0), acc[u][s]);
+      } else {
 #pragma unroll
         for (int s = 0; s < S; ++s)
 #pragma unroll
-          for (int v = 0; v < V; ++v) acc[s][v] = fmaf(b[s * BC + v], dz[q][v], acc[s][v]);
+          for (int v = 0; v < V; ++v) acc[u][s][v] = 0.f;
       }
     }
+    for (int e = 0; e < E4; e += EG) {
+      float dz[EG][U][V];
 #pragma unroll
-    for (int s = 0; s < S; ++s) store_vec<TX, V>(out + slot_offset<K>(p0, s, g, c0), acc[s]);
+      for (int q = 0; q < EG; ++q)
+#pragma unroll
+        for (int u = 0; u < U; ++u) load_vec<TW, V>(static_cast<const TW*>(upd.p[e + q]) + zoff[u], dz[q][u]);
+      load_fence();
+#pragma unroll
+      for (int q = 0; q < EG; ++q)
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            const float b = lds[lds_w<V>((e + q) * S + s, threadIdx.x, v, BCG)];
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc[u][s][v] = fmaf(b, dz[q][u][v], acc[u][s][v]);
+          }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (ok[u]) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) store_vec<TX, V>(out + slot_offset<K>(p0[u], s, g, c0), acc[u][s]);
+      }
   }
 }
 
@@ -358,61 +408,107 @@ __device__ __forceinline__ void block_reduce_rows(const float* acc, float* red, 
 // ----------------------------------------------------------------------------------
 // weight gradient partials: part[chunk][e][s][c] = sum_{m in chunk} x[m,s,c] * z_e[m,c]
 // CARRIER: x is the NHWC carrier with S = K*K slots; otherwise x is a workspace
-// [M, C] tensor (S = 1; the triangular gamma gradient). EMAX events are accumulated
-// per lane; the host pads z.p[E..EMAX) with a valid pointer and only rows e < E are
-// reduced, so the token loop has no branches.
-// block (BCG*S lanes, lane = s*BCG + cg; TL), 1-D grid (slices x chunks).
+// [M, C] tensor (S = 1; the triangular gamma gradient).
+// Block = (BCG channel groups) x (E event lanes): lane (e, cg) owns the S x V outputs
+// of event e and channel group cg, so each update element is loaded by exactly one
+// lane. The block's x tile (TT tokens x S slots x BCG*V channels) is staged in LDS once
+// and read by all E event lanes. 1-D grid (slices x chunks).
 // ----------------------------------------------------------------------------------
-template <typename T, int V, int K, int EMAX, bool CARRIER>
-__global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack z,
-                                               float* __restrict__ part,
-                                               const int32_t* __restrict__ index, int E, int BCG,
-                                               Geo g, int tpb, int nslices) {
+template <typename T, int V, int K, bool CARRIER>
+__global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack z, float* __restrict__ part,
+                                               const int32_t* __restrict__ index, int E, Geo g, int tpb,
+                                               int nslices, int TT) {
   constexpr int S = CARRIER ? K * K : 1;
-  extern __shared__ float red[];
-  const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
-  const int s = threadIdx.x / BCG;
-  const int cg = threadIdx.x - s * BCG;
+  extern __shared__ float xt[];  // [TT*S rows][BCG*V], lds_w layout
+  const int BCG = blockDim.x;
   const int BC = BCG * V;
-  const int c0 = slice * BC + cg * V;
-  float acc[EMAX][V];
-#pragma unroll
-  for (int j = 0; j < EMAX; ++j)
-#pragma unroll
-    for (int v = 0; v < V; ++v) acc[j][v] = 0.f;
-  if (c0 < g.C) {
-    const int m_begin = chunk * tpb;
-    const int m_end = min(m_begin + tpb, g.M);
-    for (int m = m_begin + threadIdx.y; m < m_end; m += blockDim.y) {
-      int64_t xoff;
-      if constexpr (CARRIER) {
-        xoff = slot_offset<K>(cell_pixel0(m, g, index), s, g, c0);
-      } else {
-        xoff = int64_t(m) * g.C + c0;
-      }
-      const int64_t zoff = int64_t(m) * g.C + c0;
-      float xv[V];
-      load_vec<T, V>(x + xoff, xv);
-      float zv[EMAX][V];
-#pragma unroll
-      for (int j = 0; j < EMAX; ++j) load_vec<T, V>(static_cast<const T*>(z.p[j]) + zoff, zv[j]);
-#pragma unroll
-      for (int j = 0; j < EMAX; ++j)
-#pragma unroll
-        for (int v = 0; v < V; ++v) acc[j][v] = fmaf(xv[v], zv[j][v], acc[j][v]);
-    }
-  }
-  float* prow = part + int64_t(chunk) * E * S * g.C;
+  const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
   const int cs = slice * BC;
+  const int cg = threadIdx.x, e = threadIdx.y;
+  const int c0 = cs + cg * V;
+  const bool active = c0 < g.C;
+  const T* __restrict__ ze = static_cast<const T*>(z.p[e]);
+  const int tid = threadIdx.y * BCG + threadIdx.x;
+  const int nthr = BCG * blockDim.y;
+  float acc[S][V];
 #pragma unroll
-  for (int j = 0; j < EMAX; ++j) {
-    if (j < E) {
-      block_reduce_rows<V>(acc[j], red, [&](int i, float sum) {
-        const int ss = i / BC;
-        const int c = cs + (i - ss * BC);
-        if (c < g.C) prow[(int64_t(j) * S + ss) * g.C + c] = sum;
-      });
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[s][v] = 0.f;
+  const int m_begin = chunk * tpb;
+  const int m_end = min(m_begin + tpb, g.M);
+  for (int t0 = m_begin; t0 < m_end; t0 += TT) {
+    // stage the x tile: rows (t, s), BCG vectors per row; 4 vectors per thread are
+    // loaded before any is stored so the loads overlap
+    const int nvec = TT * S * BCG;
+    for (int i0 = tid; i0 < nvec; i0 += 4 * nthr) {
+      float v8[4][V];
+      int dst[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int i = i0 + q * nthr;
+        const int row = min(i, nvec - 1) / BCG;
+        const int cgi = min(i, nvec - 1) - row * BCG;
+        const int t = row / S;
+        const int ss = row - t * S;
+        const int m = t0 + t;
+        const int ci = cs + cgi * V;
+        dst[q] = i < nvec ? row * BCG + cgi : -1;
+        if (m < m_end && ci < g.C) {
+          int64_t off;
+          if constexpr (CARRIER) {
+            off = slot_offset<K>(cell_pixel0(m, g, index), ss, g, ci);
+          } else {
+            off = int64_t(m) * g.C + ci;
+          }
+          load_vec<T, V>(x + off, v8[q]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < V; ++v) v8[q][v] = 0.f;
+        }
+      }
+      load_fence();
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (dst[q] >= 0) {
+          const int row = dst[q] / BCG;
+          const int cgi = dst[q] - row * BCG;
+#pragma unroll
+          for (int v = 0; v < V; ++v) xt[lds_w<V>(row, cgi, v, BCG)] = v8[q][v];
+        }
+      }
     }
+    __syncthreads();
+    if (active) {
+      const int tn = min(TT, m_end - t0);
+      for (int t = 0; t < tn; t += 8) {
+        float zv[8][V];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int tq = min(t + q, tn - 1);  // clamp: a repeated token is loaded, not added
+          load_vec<T, V>(ze + int64_t(t0 + tq) * g.C + c0, zv[q]);
+        }
+        load_fence();
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          if (t + q < tn) {
+#pragma unroll
+            for (int ss = 0; ss < S; ++ss)
+#pragma unroll
+              for (int v = 0; v < V; ++v)
+                acc[ss][v] = fmaf(xt[lds_w<V>((t + q) * S + ss, cg, v, BCG)], zv[q][v], acc[ss][v]);
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (!active) return;
+  float* prow = part + (int64_t(chunk) * E + e) * S * g.C;
+#pragma unroll
+  for (int ss = 0; ss < S; ++ss) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) prow[int64_t(ss) * g.C + c0 + v] = acc[ss][v];
   }
 }
 
@@ -475,6 +571,7 @@ template <typename T, typename TG, int V>
 __global__ void __launch_bounds__(256) k_triangular(const T* __restrict__ base, PtrPack upd,
                                                     const TG* __restrict__ gamma, T* __restrict__ out,
                                                     int A, int M, int C, int tpb, int nslices) {
+  constexpr int U = SIHC_RW_UNROLL;  // tokens per lane per iteration: each LDS weight feeds U tokens
   extern __shared__ float lds[];
   const int BCG = blockDim.x, TL = blockDim.y;
   const int BC = BCG * V;
@@ -486,31 +583,43 @@ __global__ void __launch_bounds__(256) k_triangular(const T* __restrict__ base, 
     const int j = i / BC;
     const int cl = i - j * BC;
     const int c = cs + cl;
-    lds[i] = (j < A && c < C) ? to_f32(gamma[int64_t(j) * C + c]) : 0.f;
+    const int cg = cl / V;
+    lds[lds_w<V>(j, cg, cl - cg * V, BCG)] = (j < A && c < C) ? to_f32(gamma[int64_t(j) * C + c]) : 0.f;
   }
   __syncthreads();
-  const int cl0 = threadIdx.x * V;
-  const int c0 = cs + cl0;
+  const int c0 = cs + threadIdx.x * V;
   if (c0 >= C) return;
   const int m_begin = chunk * tpb;
   const int m_end = min(m_begin + tpb, M);
-  for (int m = m_begin + threadIdx.y; m < m_end; m += TL) {
-    const int64_t off = int64_t(m) * C + c0;
-    float acc[V];
-    load_vec<T, V>(base + off, acc);
-    for (int j = 0; j < A4; j += 4) {
-      float dz[4][V];
+  for (int m = m_begin + threadIdx.y; m < m_end; m += U * TL) {
+    bool ok[U];
+    int64_t off[U];
+    float acc[U][V];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) load_vec<T, V>(static_cast<const T*>(upd.p[j + q]) + off, dz[q]);
+    for (int u = 0; u < U; ++u) {
+      ok[u] = m + u * TL < m_end;
+      off[u] = int64_t(ok[u] ? m + u * TL : m) * C + c0;
+      load_vec<T, V>(base + off[u], acc[u]);
+    }
+    for (int j = 0; j < A4; j += 4) {
+      float dz[4][U][V];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int u = 0; u < U; ++u) load_vec<T, V>(static_cast<const T*>(upd.p[j + q]) + off[u], dz[q][u]);
       load_fence();
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float* gm = lds + (j + q) * BC + cl0;
+      for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int v = 0; v < V; ++v) acc[v] = fmaf(gm[v], dz[q][v], acc[v]);
-      }
+        for (int v = 0; v < V; ++v) {
+          const float gm = lds[lds_w<V>(j + q, threadIdx.x, v, BCG)];
+#pragma unroll
+          for (int u = 0; u < U; ++u) acc[u][v] = fmaf(gm, dz[q][u][v], acc[u][v]);
+        }
     }
-    store_vec<T, V>(out + off, acc);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (ok[u]) store_vec<T, V>(out + off[u], acc[u]);
   }
 }
 
@@ -939,52 +1048,38 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
   const void* ptrs[SIHC_MAX_EVENTS + 1];
   for (int i = 0; i < events; ++i) ptrs[i] = z[i];
   ptrs[events] = x;
-  const int emax = events <= 1 ? 1 : events <= 2 ? 2 : events <= 4 ? 4 : events <= 8 ? 8 : events <= 12 ? 12
-                   : events <= 16 ? 16 : events <= 24 ? 24 : 32;
-  // At most 64 fp32 accumulators per lane (the loaded z values need as many again).
-  const int V = pick_vec(g.C, es, std::max(1, 64 / emax), ptrs, events + 1);
+  const int V = pick_vec(g.C, es, 8, ptrs, events + 1);
   const int CG = (g.C + V - 1) / V;
-  int bcg = 16;
+  // BCG channel-group lanes x `events` event lanes <= 256 threads.
+  int bcg = 64;
+  while (bcg > 1 && bcg * events > 256) bcg /= 2;
   while (bcg > 1 && bcg / 2 >= CG) bcg /= 2;
-  while (bcg * S > 256) bcg /= 2;
-  const int lanes = bcg * S;
-  const int tl = 256 / lanes;
   const int slices = (CG + bcg - 1) / bcg;
   const int tpb = int((int64_t(g.M) + chunks - 1) / chunks);
-  const size_t lds = size_t(tl) * lanes * V * sizeof(float);
+  // x tile of TT tokens: at most 32 KB of LDS.
+  int tt = 32768 / (S * bcg * V * int(sizeof(float)));
+  tt = std::max(1, std::min(tt, 32));
+  const size_t lds = size_t(tt) * S * bcg * V * sizeof(float);
   const PtrPack pk = pack(z, events);
   float* part = static_cast<float*>(workspace);
   int rc = with_dtype(dtype, [&](auto t) {
     using T = decltype(t);
     return with_vec(V, [&](auto vv) {
       constexpr int VV = decltype(vv)::value;
-      auto go = [&](auto em, auto kk, auto car) {
-        constexpr int EM = decltype(em)::value;
-        constexpr int KK = decltype(kk)::value;
-        constexpr bool CAR = decltype(car)::value;
-        if constexpr (EM * VV > 64 || VV * sizeof(T) > 16) {
-          return fail(SIHC_ERR_INVALID, "%s: internal accumulator width", what);
-        } else {
-          hipLaunchKernelGGL((k_wgrad<T, VV, KK, EM, CAR>), dim3(blocks1d(slices, chunks)), dim3(lanes, tl), lds, st,
-                             static_cast<const T*>(x), pk, part, index, events, bcg, g, tpb, slices);
+      if constexpr (VV * sizeof(T) > 16) {
+        return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
+      } else {
+        auto go = [&](auto kk, auto car) {
+          constexpr int KK = decltype(kk)::value;
+          constexpr bool CAR = decltype(car)::value;
+          hipLaunchKernelGGL((k_wgrad<T, VV, KK, CAR>), dim3(blocks1d(slices, chunks)), dim3(bcg, events), lds, st,
+                             static_cast<const T*>(x), pk, part, index, events, g, tpb, slices, tt);
           return check_launch(what);
-        }
-      };
-      auto with_em = [&](auto kk, auto car) {
-        switch (emax) {
-          case 1: return go(IC<1>{}, kk, car);
-          case 2: return go(IC<2>{}, kk, car);
-          case 4: return go(IC<4>{}, kk, car);
-          case 8: return go(IC<8>{}, kk, car);
-          case 12: return go(IC<12>{}, kk, car);
-          case 16: return go(IC<16>{}, kk, car);
-          case 24: return go(IC<24>{}, kk, car);
-          default: return go(IC<32>{}, kk, car);
-        }
-      };
-      if (!carrier) return with_em(IC<2>{}, std::false_type{});
-      if (g.K == 2) return with_em(IC<2>{}, std::true_type{});
-      return with_em(IC<4>{}, std::true_type{});
+        };
+        if (!carrier) return go(IC<2>{}, std::false_type{});
+        if (g.K == 2) return go(IC<2>{}, std::true_type{});
+        return go(IC<4>{}, std::true_type{});
+      }
     });
   });
   if (rc) return rc;
