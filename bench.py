@@ -49,6 +49,7 @@ def parse_args():
     p.add_argument("--events", type=int, default=56)
     p.add_argument("--seed", type=int, default=2)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extra", action="store_true", help="skip the secondary config 1/3 figures")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--mode", choices=("step", "calibrate", "kernels"), default="step",
                    help="step: the benchmark (default); calibrate: a 1 GiB copy-kernel launch plus single "
@@ -156,6 +157,95 @@ class LiteralStep:
     def step(self, timer=None):
         self.run(self.fwd)
         self.run(self.bwd, timer)
+
+
+def _timed(torch, fn, iters=10, warmup=2):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters * 1e-3
+
+
+def extra_configs(seed: int) -> dict:
+    """Secondary figures on BASELINE configs 1 and 3 (not the headline `value`).
+
+    config 1: SiHC-B shape (batch 256, D=768), forward only, one 24-event stage, as the
+      per-event fused schedule and as the reference's stage API (read E=24, triangular
+      with 1..23 active updates, write E=24). Sublayer outputs pre-drawn.
+    config 3: spatially indexed variant (batch 128, D=1152, group-of-5 index): the
+      per-event fused forward and backward through the index, and the explicit bit-exact
+      gather/scatter of every token's state.
+    """
+    import torch
+
+    from sihc_hip import launch
+    from sihc_hip.indexed import group_index
+
+    dev = torch.device("cuda", 0)
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(seed)
+    r = lambda shape, m=0.0, sd=1.0: (m + sd * torch.randn(shape, device=dev, generator=g)).to(bf)  # noqa: E731
+    out = {}
+    # ---- config 1
+    B, C, E, S = 256, 768, 24, 4
+    U = B * 256 * C * ELEM
+    x0 = r((B, 32, 32, C))
+    alpha = r((E, C, S), 0.25, 0.02)
+    beta = r((E, C, S), 1.0, 0.02)
+    dz = [r((B, 256, C)) for _ in range(E)]
+    gamma = (alpha[:, None].float() * beta[None, :].float()).sum(-1).to(bf)
+    xs = [x0] + [torch.empty_like(x0) for _ in range(E)]
+
+    def literal():
+        launch.read(x0, alpha[:1])
+        for i in range(E):
+            launch.event_forward(xs[i], dz[i], beta[i], alpha[i + 1] if i + 1 < E else None)
+
+    def stage():
+        base = launch.read(x0, alpha)
+        for i in range(1, E):
+            launch.triangular(base[i], dz[:i], gamma[i, :i].contiguous())
+        launch.write(x0, dz, beta)
+
+    lit_bytes = ((S + 1) + (E - 1) * (2 * S + 2) + (2 * S + 1)) * U
+    stage_bytes = ((S + E) + sum(i + 2 for i in range(1, E)) + (2 * S + E)) * U
+    t_lit, t_stage = _timed(torch, literal, iters=5), _timed(torch, stage, iters=5)
+    out["config1_forward"] = {
+        "workload": "batch 256, D=768, 24 events (12 layers x 2 sublayers), forward only, bf16",
+        "per_event_fused": {"ms": round(t_lit * 1e3, 3), "GB/s": round(lit_bytes / t_lit / 1e9, 1),
+                            "bytes": lit_bytes, "tokens_per_s": round(B * 256 / t_lit, 1)},
+        "stage_api": {"ms": round(t_stage * 1e3, 3), "GB/s": round(stage_bytes / t_stage / 1e9, 1),
+                      "bytes": stage_bytes, "tokens_per_s": round(B * 256 / t_stage, 1)},
+    }
+    del xs, dz, x0
+    torch.cuda.empty_cache()
+    # ---- config 3
+    B, C = 128, 1152
+    U = B * 256 * C * ELEM
+    x = r((B, 32, 32, C))
+    idx = group_index(B, 16, 5, seed=3).to(dev)
+    d = r((B, 256, C))
+    bw, aw = r((C, S), 1.0, 0.02), r((C, S), 0.25, 0.02)
+    xo, zo = launch.event_forward(x, d, bw, aw, index=idx)
+    h, gz = r((B, 32, 32, C), 0.0, 1e-2), r((B, 256, C), 0.0, 1e-2)
+    cells = launch.gather_cells(x, idx, S)
+    t_f = _timed(torch, lambda: launch.event_forward(x, d, bw, aw, index=idx))
+    t_b = _timed(torch, lambda: launch.event_backward(h, gz, xo, d, bw, aw, index=idx))
+    t_g = _timed(torch, lambda: launch.gather_cells(x, idx, S))
+    t_s = _timed(torch, lambda: launch.scatter_cells(cells, idx))
+    out["config3_indexed"] = {
+        "workload": "batch 128, D=1152, int32 state index (seeded groups of 5), bf16",
+        "event_forward_GB/s": round(10 * U / t_f / 1e9, 1), "event_backward_GB/s": round(15 * U / t_b / 1e9, 1),
+        "gather_GB/s": round(2 * S * U / t_g / 1e9, 1), "scatter_GB/s": round(2 * S * U / t_s / 1e9, 1),
+        "event_fwd_bwd_tokens_per_s": round(B * 256 / (t_f + t_b), 1),
+    }
+    return out
 
 
 def cpu_baseline(budget_s: float) -> dict:
@@ -304,6 +394,9 @@ def kernels(args) -> None:
     h = r((B, 32, 32, C), 0.0, 1e-2)
     cases.append(("event_backward", 15 * U,
                   lambda: launch.event_backward(h, ws[1], x, ws[0], beta[0], alpha[1])))
+    cp_src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    cp_dst = torch.empty_like(cp_src)
+    cases.append(("copy 1 GiB (read+write ceiling)", 2 << 30, lambda: launch.copy_(cp_dst, cp_src)))
     xb = x[: B // 2].contiguous()
     idx = group_index(B // 2, 16, 5, seed=3).to(dev)
     cells = launch.gather_cells(xb, idx, S)
@@ -407,6 +500,11 @@ def main():
             "launches": len(kern_ms),
         },
     }
+    if not args.no_extra:
+        del step
+        torch.cuda.empty_cache()
+        print("[bench] secondary configs 1 and 3", file=sys.stderr, flush=True)
+        result["extra"] = extra_configs(args.seed)
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
