@@ -1,0 +1,136 @@
+"""GPU: the HIP-backed ops under fullgraph torch.compile and HIP-graph capture.
+
+Mirrors the reference's compile and graph contracts (research/tests/
+test_sublayer_kernels.py:187-213, :268-286; test_runtime_compatibility.py:102-151):
+the custom ops trace through their fake implementations with no graph break, their
+autograd rules run under AOTAutograd, and captured launches replay correctly. The
+compile backend is aot_eager (tracing, functionalisation and AOT autograd without
+generating any kernels), so the only device code that runs is this library's.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from helpers import announce, assert_parity
+from sihc_hip.event_ops import event_write_read, literal_stage
+from sihc_hip.sublayer_kernels import sublayer_read, sublayer_triangular, sublayer_write
+
+pytestmark = pytest.mark.gpu
+
+
+def stage(x, alpha, beta):
+    """The reference's fused stage schedule (sublayer.py:52-72) with tanh bodies."""
+    events = alpha.shape[0]
+    base = sublayer_read(x, alpha)
+    gamma = (alpha[:, None] * beta[None, :]).sum(-1)
+    updates = []
+    for i in range(events):
+        z = base[i] if i == 0 else sublayer_triangular(base[i], updates, gamma[i, :i].contiguous())
+        updates.append((0.05 * torch.tanh(z)).contiguous())
+    return sublayer_write(x, updates, beta)
+
+
+def _inputs(dtype, events=8, slots=4, c=64, seed=0):
+    torch.manual_seed(seed)
+    k = 2 if slots == 4 else 4
+    x = torch.randn(2, 4 * k, 4 * k, c, device="cuda", dtype=dtype)
+    alpha = (0.25 + 0.05 * torch.randn(events, c, slots, device="cuda")).to(dtype)
+    beta = (1.0 + 0.05 * torch.randn(events, c, slots, device="cuda")).to(dtype)
+    return x, alpha, beta
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fullgraph_compile_of_stage_forward_backward(dtype):
+    announce(f"compile stage dtype={dtype}")
+    torch._dynamo.reset()
+    x, alpha, beta = _inputs(dtype)
+    leaves = [t.clone().requires_grad_() for t in (x, alpha, beta)]
+    eager = stage(*leaves)
+    go = torch.randn_like(eager) * 0.1
+    ge = torch.autograd.grad(eager, leaves, go)
+    compiled = torch.compile(stage, backend="aot_eager", fullgraph=True)
+    leaves2 = [t.clone().requires_grad_() for t in (x, alpha, beta)]
+    out = compiled(*leaves2)
+    gc = torch.autograd.grad(out, leaves2, go)
+    assert torch.equal(out, eager)
+    for a, b in zip(gc, ge):
+        assert_parity(a, b, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fullgraph_compile_of_literal_stage(dtype):
+    announce(f"compile literal dtype={dtype}")
+    torch._dynamo.reset()
+    x, alpha, beta = _inputs(dtype, events=5)
+    fns = [lambda z, i=i: 0.1 * torch.tanh((1 + 0.1 * i) * z) for i in range(5)]
+
+    def fn(x, a, b):
+        return literal_stage(x, a, b, fns)
+
+    leaves = [t.clone().requires_grad_() for t in (x, alpha, beta)]
+    eager = fn(*leaves)
+    go = torch.randn_like(eager) * 0.1
+    ge = torch.autograd.grad(eager, leaves, go)
+    leaves2 = [t.clone().requires_grad_() for t in (x, alpha, beta)]
+    out = torch.compile(fn, backend="aot_eager", fullgraph=True)(*leaves2)
+    gc = torch.autograd.grad(out, leaves2, go)
+    assert torch.equal(out, eager)
+    for a, b in zip(gc, ge):
+        assert_parity(a, b, dtype)
+
+
+def test_hip_graph_capture_and_replay_of_stage_forward():
+    announce("hip graph stage forward")
+    x, alpha, beta = _inputs(torch.bfloat16, events=12, seed=1)
+    static_x = x.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm up allocations outside the capture
+        for _ in range(2):
+            stage(static_x, alpha, beta)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = stage(static_x, alpha, beta)
+    for r in range(4):
+        fresh = torch.randn_like(x) * (1 + r)
+        static_x.copy_(fresh)
+        graph.replay()
+        # eager work and a synchronisation between replays
+        expected = stage(fresh, alpha, beta)
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, expected), f"replay {r} differs from eager"
+
+
+def test_hip_graph_capture_of_event_backward_chain():
+    announce("hip graph event fwd+bwd")
+    x, alpha, beta = _inputs(torch.bfloat16, events=3, seed=2)
+    dz = torch.randn(2, 16, 64, device="cuda", dtype=torch.bfloat16)
+    static = [t.clone().requires_grad_() for t in (x, dz)]
+    g_x = 1e-2 * torch.randn_like(x)
+    g_z = 1e-2 * torch.randn_like(dz)
+
+    def run(xx, dd):
+        # upstream gradients are given, so no reduction kernel is captured
+        xo, zo = event_write_read(xx, dd, beta[0], alpha[1])
+        return torch.autograd.grad((xo, zo), (xx, dd), (g_x, g_z))
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            run(*static)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gx, gd = run(*static)
+    for r in range(3):
+        nx, nd = torch.randn_like(x), torch.randn_like(dz)
+        with torch.no_grad():
+            static[0].copy_(nx)
+            static[1].copy_(nd)
+        graph.replay()
+        ex, ed = run(nx.clone().requires_grad_(), nd.clone().requires_grad_())
+        torch.cuda.synchronize()
+        assert torch.equal(gx, ex) and torch.equal(gd, ed), f"replay {r} differs from eager"
