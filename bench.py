@@ -49,12 +49,15 @@ def parse_args():
     p.add_argument("--events", type=int, default=56)
     p.add_argument("--seed", type=int, default=2)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--no-extra", action="store_true", help="skip the secondary config 1/3 figures")
+    p.add_argument("--no-extra", action="store_true", help="skip the secondary config 1/3/4 figures")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
-    p.add_argument("--mode", choices=("step", "calibrate", "kernels"), default="step",
+    p.add_argument("--schedule", choices=("stage", "literal"), default="stage",
+                   help="routing schedule of --mode e2e")
+    p.add_argument("--mode", choices=("step", "calibrate", "kernels", "e2e"), default="step",
                    help="step: the benchmark (default); calibrate: a 1 GiB copy-kernel launch plus single "
                         "event forward/backward launches at the same shape, for HBM counter runs; kernels: "
-                        "every HIP kernel timed alone at the benchmark shape (one JSON line per kernel)")
+                        "every HIP kernel timed alone at the benchmark shape (one JSON line per kernel); e2e: "
+                        "BASELINE config 4, a SiHC-XL denoiser forward on a CFG batch with HIP routing")
     return p.parse_args()
 
 
@@ -409,6 +412,54 @@ def kernels(args) -> None:
               flush=True)
 
 
+def e2e_config4(seed: int, schedules=("stage", "literal"), steps: int = 5) -> dict:
+    """SiHC-XL sublayer denoiser (p8, D=1152, 28 blocks, 16 heads,
+    MLP ratio 4, stages 8/12/8), bf16, random init; one forward of 64 class-conditional
+    + 64 unconditional (label 1000) samples from N(0,1) images, t ~ U(0,1). Routing on
+    the HIP ops; bodies on PyTorch-ROCm. Reports samples/s, images/s per CFG step and
+    the share of the forward spent in routing (HIP events around each routing call)."""
+    import torch
+
+    from sihc_hip.e2e import SiHCDenoiser
+
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(seed)
+    model = SiHCDenoiser().random_init(seed=seed).to(dev, torch.bfloat16).eval()
+    x = torch.randn(128, 3, 256, 256, device=dev).to(torch.bfloat16)
+    t = torch.rand(128, device=dev)
+    y = torch.cat([torch.randint(0, 1000, (64,), device=dev), torch.full((64,), 1000, device=dev)])
+    out = {"workload": "BASELINE config 4: SiHC-XL sublayer denoiser forward, CFG batch 64+64, bf16, random init"}
+    for schedule in schedules:
+        model.schedule = schedule
+        with torch.no_grad():
+            for _ in range(2):
+                model(x, t, y)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                y_hat = model(x, t, y)
+            torch.cuda.synchronize()
+            fwd = (time.perf_counter() - t0) / steps
+            model.routing_timer = []
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            model(x, t, y)
+            b.record()
+            torch.cuda.synchronize()
+            routing = sum(s.elapsed_time(e) for s, e in model.routing_timer) * 1e-3
+            total = a.elapsed_time(b) * 1e-3
+            model.routing_timer = None
+        assert torch.isfinite(y_hat.float()).all(), "non-finite output"
+        out[schedule] = {"forward_ms": round(fwd * 1e3, 3), "samples_per_s": round(128 / fwd, 1),
+                         "images_per_s_per_cfg_step": round(64 / fwd, 1), "routing_ms": round(routing * 1e3, 3),
+                         "routing_share": round(routing / total, 4)}
+    return out
+
+
+def e2e(args) -> None:
+    print(json.dumps(e2e_config4(args.seed, (args.schedule,), max(1, min(args.steps, 10)))), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -426,6 +477,9 @@ def main():
         return
     if args.mode == "kernels":
         kernels(args)
+        return
+    if args.mode == "e2e":
+        e2e(args)
         return
     print(f"[bench] building step: batch={args.batch} C={args.channels} events={args.events}", file=sys.stderr,
           flush=True)
@@ -505,6 +559,9 @@ def main():
         torch.cuda.empty_cache()
         print("[bench] secondary configs 1 and 3", file=sys.stderr, flush=True)
         result["extra"] = extra_configs(args.seed)
+        torch.cuda.empty_cache()
+        print("[bench] config 4 end-to-end forward", file=sys.stderr, flush=True)
+        result["extra"]["config4_e2e"] = e2e_config4(args.seed)
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
