@@ -364,6 +364,15 @@ __global__ void __launch_bounds__(256) k_write(const TX* __restrict__ x, PtrPack
 #pragma unroll
         for (int u = 0; u < U; ++u) load_vec<TW, V>(static_cast<const TW*>(upd.p[e + q]) + zoff[u], dz[q][u]);
       load_fence();
+      // Padded events (e + q >= E) loaded a repeated real update: zero the values
+      // themselves (a zero weight times an Inf would still give NaN).
+#pragma unroll
+      for (int q = 0; q < EG; ++q)
+        if (e + q >= E)
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int v = 0; v < V; ++v) dz[q][u][v] = 0.f;
 #pragma unroll
       for (int q = 0; q < EG; ++q)
 #pragma unroll
@@ -610,6 +619,13 @@ __global__ void __launch_bounds__(256) k_triangular(const T* __restrict__ base, 
       load_fence();
 #pragma unroll
       for (int q = 0; q < 4; ++q)
+        if (j + q >= A)  // padded update: zero the loaded values (0 * Inf is NaN)
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int v = 0; v < V; ++v) dz[q][u][v] = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int v = 0; v < V; ++v) {
           const float gm = lds[lds_w<V>(j + q, threadIdx.x, v, BCG)];
@@ -730,7 +746,7 @@ __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_bwd(const T* __rest
       int64_t p0[U], zoff[U];
       bool ok[U];
       float gz[U][V], d[U][V], t[U][S][V], xv[U][S][V];
-      // ---- loads (tail tokens reload a valid token; their gz/d are zeroed below so
+      // ---- loads (tail tokens reload a valid token; their values are zeroed below so
       //      they add nothing to the weight gradients, and nothing is stored)
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -757,11 +773,20 @@ __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_bwd(const T* __rest
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (U > 1 && !ok[u]) {
+          // tail token: zero every loaded value so it adds exactly nothing (a zero
+          // factor alone would turn an Inf in the repeated token into NaN)
 #pragma unroll
           for (int v = 0; v < V; ++v) {
             gz[u][v] = 0.f;
             d[u][v] = 0.f;
           }
+#pragma unroll
+          for (int ss = 0; ss < S; ++ss)
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              t[u][ss][v] = 0.f;
+              xv[u][ss][v] = 0.f;
+            }
         }
         float gd[V];
 #pragma unroll
@@ -929,6 +954,12 @@ int check_geometry(const char* what, int64_t batch, int grid, int cell, int chan
   return SIHC_OK;
 }
 
+int check_count(const char* what, int events) {
+  if (events < 1 || events > SIHC_MAX_EVENTS)
+    return fail(SIHC_ERR_INVALID, "%s: events must be in 1..%d, got %d", what, SIHC_MAX_EVENTS, events);
+  return SIHC_OK;
+}
+
 int check_events(const char* what, int events, const void* const* ptrs) {
   if (events < 1 || events > SIHC_MAX_EVENTS)
     return fail(SIHC_ERR_INVALID, "%s: events must be in 1..%d, got %d", what, SIHC_MAX_EVENTS, events);
@@ -1003,8 +1034,8 @@ int cells_copy(const char* what, bool gather, const void* src, const int32_t* in
   Geo g;
   if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
   if (!valid_dtype(dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype %d", what, dtype);
+  if (g.M == 0) return SIHC_OK;  // empty tensors may carry NULL data pointers
   if (!src || !dst) return fail(SIHC_ERR_INVALID, "%s: null pointer", what);
-  if (g.M == 0) return SIHC_OK;
   const int64_t row_bytes = int64_t(channels) * elem_size(dtype);
   const int S = cell * cell;
   const int64_t rows = int64_t(g.M) * S;
@@ -1108,9 +1139,10 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
   Geo g;
   if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
   if (!valid_dtype(dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype %d", what, dtype);
+  if (int rc = check_count(what, events)) return rc;
+  if (g.M == 0) return SIHC_OK;  // empty tensors may carry NULL data pointers
   if (!x || !alpha) return fail(SIHC_ERR_INVALID, "%s: null input", what);
   if (int rc = check_events(what, events, const_cast<const void* const*>(out))) return rc;
-  if (g.M == 0) return SIHC_OK;
   const int es = elem_size(dtype);
   const void* ptrs[SIHC_MAX_EVENTS + 1];
   for (int i = 0; i < events; ++i) ptrs[i] = out[i];
@@ -1151,9 +1183,10 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
   if (!valid_dtype(x_dtype) || !valid_dtype(w_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
   if (x_dtype == SIHC_DTYPE_BF16 && w_dtype == SIHC_DTYPE_F32)
     return fail(SIHC_ERR_INVALID, "%s: fp32 updates with a bf16 carrier are not supported", what);
+  if (int rc = check_count(what, events)) return rc;
+  if (g.M == 0) return SIHC_OK;  // empty tensors may carry NULL data pointers
   if ((add_x && !x) || !beta || !out) return fail(SIHC_ERR_INVALID, "%s: null input", what);
   if (int rc = check_events(what, events, updates)) return rc;
-  if (g.M == 0) return SIHC_OK;
   const void* ptrs[SIHC_MAX_EVENTS + 2];
   for (int i = 0; i < events; ++i) ptrs[i] = updates[i];
   ptrs[events] = add_x ? x : nullptr;
@@ -1207,11 +1240,13 @@ int sihc_weight_grad(const void* x, const void* const* z, void* out, int events,
   Geo g;
   if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
   if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
-  if (!x || !out) return fail(SIHC_ERR_INVALID, "%s: null input", what);
-  if (int rc = check_events(what, events, z)) return rc;
+  if (int rc = check_count(what, events)) return rc;
+  if (!out) return fail(SIHC_ERR_INVALID, "%s: null output", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (g.M == 0)  // empty reduction: zero gradient
+  if (g.M == 0)  // empty reduction: zero gradient (inputs may carry NULL pointers)
     return fill_zero(out_dtype, out, int64_t(events) * cell * cell * channels, st, what);
+  if (!x) return fail(SIHC_ERR_INVALID, "%s: null input", what);
+  if (int rc = check_events(what, events, z)) return rc;
   return launch_wgrad(what, x, z, out, events, g, cell * cell, true, index, dtype, out_dtype, workspace,
                       workspace_bytes, st);
 }
@@ -1221,9 +1256,10 @@ int sihc_triangular(const void* base, const void* const* updates, const void* ga
   const char* what = "sihc_triangular";
   if (rows < 0 || rows >= (int64_t(1) << 31) || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
   if (!valid_dtype(dtype) || !valid_dtype(gamma_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
+  if (int rc = check_count(what, active)) return rc;
+  if (rows == 0) return SIHC_OK;  // empty tensors may carry NULL data pointers
   if (!base || !gamma || !out) return fail(SIHC_ERR_INVALID, "%s: null input", what);
   if (int rc = check_events(what, active, updates)) return rc;
-  if (rows == 0) return SIHC_OK;
   const int es = elem_size(dtype);
   const void* ptrs[SIHC_MAX_EVENTS + 2];
   for (int i = 0; i < active; ++i) ptrs[i] = updates[i];
@@ -1267,10 +1303,12 @@ int sihc_triangular_gamma_grad(const void* grad, const void* const* updates, voi
   const char* what = "sihc_triangular_gamma_grad";
   if (rows < 0 || rows >= (int64_t(1) << 31) || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
   if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
-  if (!grad || !out) return fail(SIHC_ERR_INVALID, "%s: null input", what);
-  if (int rc = check_events(what, active, updates)) return rc;
+  if (int rc = check_count(what, active)) return rc;
+  if (!out) return fail(SIHC_ERR_INVALID, "%s: null output", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (rows == 0) return fill_zero(out_dtype, out, int64_t(active) * channels, st, what);
+  if (!grad) return fail(SIHC_ERR_INVALID, "%s: null input", what);
+  if (int rc = check_events(what, active, updates)) return rc;
   Geo g;
   g.M = int(rows);
   g.GG = 1;
@@ -1289,10 +1327,10 @@ int sihc_event_forward(const void* x, const void* dz, const void* beta, const vo
   Geo g;
   if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
   if (!valid_dtype(dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
+  if (g.M == 0) return SIHC_OK;  // empty tensors may carry NULL data pointers
   if (!x || !dz || !beta || !x_out) return fail(SIHC_ERR_INVALID, "%s: null input", what);
   if ((alpha_next == nullptr) != (z_out == nullptr))
     return fail(SIHC_ERR_INVALID, "%s: alpha_next and z_out must both be given or both be NULL", what);
-  if (g.M == 0) return SIHC_OK;
   const int es = elem_size(dtype);
   const int S = cell * cell;
   if (!aligned(beta, std::min(16, S * es)) || (alpha_next && !aligned(alpha_next, std::min(16, S * es))))
@@ -1345,6 +1383,15 @@ int sihc_event_backward(const void* grad_x_out, const void* grad_z_out, const vo
   Geo g;
   if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
   if (!valid_dtype(dtype) || !valid_dtype(w_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
+  const int S = cell * cell;
+  const int64_t wn = int64_t(S) * channels;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (g.M == 0) {  // no tokens: zero weight gradients (token tensors may carry NULL pointers)
+    if (beta && grad_beta)
+      if (int rc = fill_zero(w_dtype, grad_beta, wn, st, what)) return rc;
+    if (grad_alpha_next) return fill_zero(w_dtype, grad_alpha_next, wn, st, what);
+    return SIHC_OK;
+  }
   const bool has_w = beta != nullptr;
   const bool has_g = grad_z_out != nullptr;
   const bool has_h = grad_x_out != nullptr;
@@ -1355,15 +1402,6 @@ int sihc_event_backward(const void* grad_x_out, const void* grad_z_out, const vo
   if (!has_w && !has_g) return fail(SIHC_ERR_INVALID, "%s: neither a write nor a read part", what);
   if (!grad_x && has_g)
     return fail(SIHC_ERR_INVALID, "%s: grad_x may be NULL only without grad_z_out (it equals grad_x_out)", what);
-  const int S = cell * cell;
-  const int64_t wn = int64_t(S) * channels;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (g.M == 0) {
-    if (has_w)
-      if (int rc = fill_zero(w_dtype, grad_beta, wn, st, what)) return rc;
-    if (grad_alpha_next) return fill_zero(w_dtype, grad_alpha_next, wn, st, what);
-    return SIHC_OK;
-  }
   const int chunks = event_bwd_chunks(g.M);
   const size_t need = size_t(chunks) * 2 * S * channels * sizeof(float);
   if (!workspace || workspace_bytes < need)

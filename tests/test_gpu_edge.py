@@ -1,0 +1,113 @@
+"""GPU edge cases: empty batches, NaN/Inf propagation, misaligned (but packed) views
+that force the scalar path, and the 16-slot cell at a larger shape."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from helpers import announce, assert_parity
+from oracle import sihc_oracle as O
+from sihc_hip import launch
+from sihc_hip.sublayer_kernels import sublayer_read, sublayer_triangular, sublayer_write
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_empty_batch(dtype):
+    announce(f"empty batch dtype={dtype}")
+    x = torch.empty(0, 32, 32, 64, device="cuda", dtype=dtype, requires_grad=True)
+    a = torch.randn(3, 64, 4, device="cuda", dtype=dtype, requires_grad=True)
+    b = torch.randn(3, 64, 4, device="cuda", dtype=dtype, requires_grad=True)
+    zs = sublayer_read(x, a)
+    assert all(z.shape == (0, 256, 64) for z in zs)
+    out = sublayer_write(x, [z.detach().requires_grad_() for z in zs], b)
+    assert out.shape == x.shape
+    ga, = torch.autograd.grad(sum(z.sum() for z in zs), (a,))
+    assert ga.shape == a.shape and torch.count_nonzero(ga) == 0
+    assert torch.count_nonzero(launch.weight_grad(x.detach(), [zz.detach() for zz in zs], b)) == 0
+    base = torch.empty(0, 256, 64, device="cuda", dtype=dtype)
+    assert sublayer_triangular(base, [base], torch.ones(1, 64, device="cuda")).shape == base.shape
+    gg = launch.triangular_gamma_grad(base, [base, base], torch.ones(2, 64, device="cuda", dtype=dtype))
+    assert torch.count_nonzero(gg) == 0
+    beta1 = torch.randn(64, 4, device="cuda", dtype=dtype)
+    xo, zo = launch.event_forward(x.detach(), base, beta1, beta1)
+    assert xo.shape == x.shape and zo.shape == base.shape
+    gx, gdz, gb, gaa = launch.event_backward(None, base, xo, base, beta1, beta1)
+    assert torch.count_nonzero(gb) == 0 and torch.count_nonzero(gaa) == 0
+
+
+def test_nan_and_inf_propagate_like_the_oracle():
+    announce("nan/inf propagation")
+    torch.manual_seed(3)
+    x = torch.randn(2, 8, 8, 64, device="cuda")
+    x[0, 0, 0, 3] = float("nan")
+    x[1, 5, 6, 10] = float("inf")
+    a = torch.randn(2, 64, 4, device="cuda")
+    ups = [torch.randn(2, 16, 64, device="cuda") for _ in range(2)]
+    ups[1][0, 2, 7] = float("-inf")
+    for got, exp in zip(sublayer_read(x, a), O.read(x.cpu(), a.cpu())):
+        assert torch.equal(torch.isnan(got).cpu(), torch.isnan(exp))
+        assert torch.equal(torch.isinf(got).cpu(), torch.isinf(exp))
+    got, exp = sublayer_write(x, ups, a), O.write(x.cpu(), [u.cpu() for u in ups], a.cpu())
+    assert torch.equal(torch.isnan(got).cpu(), torch.isnan(exp))
+    assert torch.equal(torch.isinf(got).cpu(), torch.isinf(exp))
+    fin = torch.isfinite(exp)
+    assert torch.allclose(got.cpu()[fin], exp[fin], rtol=1e-5, atol=1e-5)
+    # bf16 NaN is stored as the canonical quiet NaN, as torch's own conversion does
+    xb = x.to(torch.bfloat16)
+    zb = sublayer_read(xb, a.to(torch.bfloat16))[0]
+    nan_bits = zb.view(torch.int16)[torch.isnan(zb)]
+    assert nan_bits.numel() > 0 and torch.all(nan_bits == torch.tensor(0x7FC0, dtype=torch.int16, device="cuda"))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_misaligned_packed_views_take_the_scalar_path(dtype):
+    # Contiguous tensors at an odd element offset: no vector width is legal, every
+    # kernel must fall back to one element per lane and stay exact.
+    announce(f"misaligned views dtype={dtype}")
+    torch.manual_seed(4)
+    c = 64
+    buf = torch.randn(2 * 8 * 8 * c + 1, device="cuda", dtype=dtype)
+    x = buf[1:].view(2, 8, 8, c)
+    assert x.is_contiguous() and x.data_ptr() % 16 != 0
+    a = (0.25 + 0.05 * torch.randn(3, c, 4, device="cuda")).to(dtype)
+    zb = torch.randn(3 * 2 * 16 * c + 1, device="cuda", dtype=dtype)
+    ups = [zb[1 + i * 2 * 16 * c: 1 + (i + 1) * 2 * 16 * c].view(2, 16, c) for i in range(3)]
+    for got, exp in zip(sublayer_read(x, a), O.read(x.cpu(), a.cpu())):
+        assert_parity(got, exp, dtype, what="read")
+    assert_parity(sublayer_write(x, ups, a), O.write(x.cpu(), [u.cpu() for u in ups], a.cpu()), dtype, what="write")
+    assert_parity(launch.weight_grad(x, ups, a), O.weight_grad(x.cpu(), [u.cpu() for u in ups], 4).to(dtype), dtype,
+                  what="weight grad")
+    g = torch.randn(2, c, device="cuda")
+    assert_parity(sublayer_triangular(ups[0], ups[1:], g),
+                  O.triangular_torch(ups[0].cpu(), [u.cpu() for u in ups[1:]], g.cpu()), dtype, what="triangular")
+    xo, zo = launch.event_forward(x, ups[0], a[0], a[1])
+    rx, rz = O.event_forward(x.cpu(), ups[0].cpu(), a[0].cpu(), a[1].cpu())
+    assert_parity(xo, rx, dtype, what="event x_out")
+    assert_parity(zo, rz, dtype, what="event z_out")
+
+
+def test_sixteen_slot_cells_at_batch_32():
+    # p4 geometry (4x4 cells, 64x64 carrier) at a larger shape: read, write and the
+    # per-event pair against the oracle on batch slices.
+    announce("p4 batch 32")
+    torch.manual_seed(5)
+    bf = torch.bfloat16
+    x = torch.randn(32, 64, 64, 256, device="cuda").to(bf)
+    a = (1 / 16 + 0.01 * torch.randn(12, 256, 16, device="cuda")).to(bf)
+    b = (1.0 + 0.02 * torch.randn(12, 256, 16, device="cuda")).to(bf)
+    zs = sublayer_read(x, a)
+    ref = O.read(x[:2].cpu(), a.cpu())
+    for e in (0, 11):
+        assert_parity(zs[e][:2], ref[e], bf, what=f"p4 read {e}")
+    ups = [torch.randn(32, 256, 256, device="cuda").to(bf) for _ in range(12)]
+    out = sublayer_write(x, ups, b)
+    assert_parity(out[-2:], O.write(x[-2:].cpu(), [u[-2:].cpu() for u in ups], b.cpu()), bf, what="p4 write")
+    xo, zo = launch.event_forward(x, ups[0], b[0], a[1])
+    rx, rz = O.event_forward(x[:2].cpu(), ups[0][:2].cpu(), b[0].cpu(), a[1].cpu())
+    assert_parity(xo[:2], rx, bf, what="p4 event x_out")
+    assert_parity(zo[:2], rz, bf, what="p4 event z_out")
+    wg = launch.weight_grad(x, ups, a)
+    exp = O.weight_grad(x[:, :, :, :32].cpu(), [u[:, :, :32].cpu() for u in ups], 16)
+    assert_parity(wg[:, :32], exp.to(bf), bf, what="p4 weight grad (channel slice)")
