@@ -393,6 +393,9 @@ def kernels(args) -> None:
     for a in (12, 23):
         cases.append((f"triangular_gamma_grad A={a}", (a + 1) * U,
                       lambda a=a: launch.triangular_gamma_grad(ws[24], ws[:a], gamma[:a])))
+    for a in (1, 11, 23):
+        cases.append((f"triangular_backward A={a}", (2 * a + 1) * U,
+                      lambda a=a: launch.triangular_backward(ws[24], ws[:a], gamma[:a])))
     cases.append(("event_forward", 10 * U, lambda: launch.event_forward(x, ws[0], beta[0], alpha[1])))
     h = r((B, 32, 32, C), 0.0, 1e-2)
     cases.append(("event_backward", 15 * U,

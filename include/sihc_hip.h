@@ -94,6 +94,19 @@ int sihc_triangular_gamma_grad(const void *grad, const void *const *updates, voi
                                int out_dtype, void *workspace, size_t workspace_bytes,
                                void *stream);
 
+/* Whole adjoint of sihc_triangular except the identity to base, in one pass over grad:
+ * grad_updates[j][m,c] = grad[m,c] * gamma[j,c] (fp32 product stored in dtype) and
+ * grad_gamma[j,c] = sum_m grad[m,c] * updates_j[m,c] (as sihc_triangular_gamma_grad,
+ * stored in out_dtype). Workspace: sihc_triangular_gamma_grad_workspace_size.
+ * Replaces: sihc/models/sihc/kernels.py:1899-1950 (`..._b4_12_ptr_active{n}_grad_fused`,
+ * kernel at :1095) and :2112-2162 (the 8-block family); also the elementwise update
+ * gradients plus `_tri_gamma_backward` of sublayer_kernels.py:369-379. */
+int sihc_triangular_backward(const void *grad, const void *const *updates, const void *gamma,
+                             void *const *grad_updates, void *grad_gamma, int active,
+                             int64_t rows, int channels, int dtype, int gamma_dtype,
+                             int out_dtype, void *workspace, size_t workspace_bytes,
+                             void *stream);
+
 /* One connection event of the literal per-event recurrence, fused into one pass:
  *   x_out[m,s,c] = x[m,s,c] + beta[c,s] * dz[m,c]                 (write + residual add)
  *   z_out[m,c]   = sum_s alpha_next[c,s] * x_out[m,s,c]            (next event's read,

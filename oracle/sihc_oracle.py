@@ -132,6 +132,27 @@ def triangular_gamma_grad(grad: Tensor, updates: Sequence[Tensor]) -> Tensor:
     return torch.stack([(g * u.double().reshape(-1, g.shape[1])).sum(0) for u in updates]).float()
 
 
+def triangular_backward(grad: Tensor, updates: Sequence[Tensor], gamma: Tensor) -> tuple[list[Tensor], Tensor]:
+    """(update gradients, fp32 [A,C] gamma gradient) of triangular_torch.
+
+    Update gradient j = fp32 grad * gamma_j cast to grad's dtype
+    (sublayer_kernels.py:369-379; the fused kernel of kernels.py:1095-1186 stores the
+    same products).
+    """
+    ddz = [(_acc(grad) * _acc(gamma[j])).to(grad.dtype) for j in range(len(updates))]
+    return ddz, triangular_gamma_grad(grad, updates)
+
+
+def cell_mean(x: Tensor, slots: int = 16) -> Tensor:
+    """[B,G*G,C]: fp32 sum of each cell's pixels in slot order, times 1/S, cast to x's
+    dtype (kernels.py:36-67, `_cell_mean_b4_fwd_kernel`)."""
+    cells = high_to_cells(x, slots)
+    acc = torch.zeros(cells[:, :, 0].shape, dtype=_acc(x).dtype)
+    for s in range(slots):
+        acc = acc + _acc(cells[:, :, s])
+    return (acc * (1.0 / slots)).to(x.dtype)
+
+
 def gamma_matrix(alpha: Tensor, beta: Tensor) -> Tensor:
     """gamma[i,j,c] = sum_s alpha_i[c,s] beta_j[c,s] (sublayer.py:60, README.md:45)."""
     return (alpha[:, None] * beta[None, :]).sum(dim=-1)

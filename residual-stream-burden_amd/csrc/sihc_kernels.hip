@@ -418,16 +418,21 @@ __device__ __forceinline__ void block_reduce_rows(const float* acc, float* red, 
 // weight gradient partials: part[chunk][e][s][c] = sum_{m in chunk} x[m,s,c] * z_e[m,c]
 // CARRIER: x is the NHWC carrier with S = K*K slots; otherwise x is a workspace
 // [M, C] tensor (S = 1; the triangular gamma gradient).
+// STORE_D (workspace mode only): also write d_e[m,c] = x[m,c] * gamma[e,c] (the
+// triangular update gradients) from the staged x tile, so one pass reads x once, each
+// z_e once and writes each d_e once.
 // Block = (BCG channel groups) x (E event lanes): lane (e, cg) owns the S x V outputs
 // of event e and channel group cg, so each update element is loaded by exactly one
 // lane. The block's x tile (TT tokens x S slots x BCG*V channels) is staged in LDS once
 // and read by all E event lanes. 1-D grid (slices x chunks).
 // ----------------------------------------------------------------------------------
-template <typename T, int V, int K, bool CARRIER>
+template <typename T, int V, int K, bool CARRIER, bool STORE_D>
 __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack z, float* __restrict__ part,
                                                const int32_t* __restrict__ index, int E, Geo g, int tpb,
-                                               int nslices, int TT) {
+                                               int nslices, int TT, PtrPack dout, const void* __restrict__ gam,
+                                               int gam_f32) {
   constexpr int S = CARRIER ? K * K : 1;
+  static_assert(!(STORE_D && CARRIER), "update gradients exist only in workspace mode");
   extern __shared__ float xt[];  // [TT*S rows][BCG*V], lds_w layout
   const int BCG = blockDim.x;
   const int BC = BCG * V;
@@ -444,6 +449,16 @@ __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack 
   for (int s = 0; s < S; ++s)
 #pragma unroll
     for (int v = 0; v < V; ++v) acc[s][v] = 0.f;
+  float gv[V];
+  T* __restrict__ de = nullptr;
+  if constexpr (STORE_D) {
+    de = static_cast<T*>(const_cast<void*>(dout.p[e]));
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int64_t gi = int64_t(e) * g.C + min(c0 + v, g.C - 1);
+      gv[v] = gam_f32 ? static_cast<const float*>(gam)[gi] : to_f32(static_cast<const bf16_t*>(gam)[gi]);
+    }
+  }
   const int m_begin = chunk * tpb;
   const int m_end = min(m_begin + tpb, g.M);
   for (int t0 = m_begin; t0 < m_end; t0 += TT) {
@@ -506,6 +521,12 @@ __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack 
 #pragma unroll
               for (int v = 0; v < V; ++v)
                 acc[ss][v] = fmaf(xt[lds_w<V>((t + q) * S + ss, cg, v, BCG)], zv[q][v], acc[ss][v]);
+            if constexpr (STORE_D) {
+              float d[V];
+#pragma unroll
+              for (int v = 0; v < V; ++v) d[v] = xt[lds_w<V>(t + q, cg, v, BCG)] * gv[v];
+              store_vec<T, V>(de + int64_t(t0 + t + q) * g.C + c0, d);
+            }
           }
         }
       }
@@ -513,6 +534,83 @@ __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack 
     __syncthreads();
   }
   if (!active) return;
+  float* prow = part + (int64_t(chunk) * E + e) * S * g.C;
+#pragma unroll
+  for (int ss = 0; ss < S; ++ss) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) prow[int64_t(ss) * g.C + c0 + v] = acc[ss][v];
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// Same partial rows as k_wgrad for one or two event lanes, where the shared x tile has
+// no reuse to pay for its staging: every lane loads its own x and z_e vectors straight
+// from memory, TG tokens per round with all loads issued before the first use, and no
+// LDS or barriers. Workspace mode and the 4-slot carrier only (16-slot accumulators
+// would not fit the registers beside TG tokens of x).
+// ----------------------------------------------------------------------------------
+template <typename T, int V, int K, bool CARRIER, bool STORE_D>
+__global__ void __launch_bounds__(256) k_wgrad_direct(const T* __restrict__ x, PtrPack z, float* __restrict__ part,
+                                                      const int32_t* __restrict__ index, int E, Geo g, int tpb,
+                                                      int nslices, PtrPack dout, const void* __restrict__ gam,
+                                                      int gam_f32) {
+  constexpr int S = CARRIER ? K * K : 1;
+  constexpr int TG = CARRIER ? 2 : 4;
+  static_assert(!(STORE_D && CARRIER), "update gradients exist only in workspace mode");
+  static_assert(S <= 4, "direct path is for the 4-slot carrier and the workspace");
+  const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
+  const int e = threadIdx.y;
+  const int c0 = (slice * blockDim.x + threadIdx.x) * V;
+  if (c0 >= g.C) return;  // no barriers below
+  const T* __restrict__ ze = static_cast<const T*>(z.p[e]);
+  float acc[S][V];
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[s][v] = 0.f;
+  float gv[V];
+  T* __restrict__ de = nullptr;
+  if constexpr (STORE_D) {
+    de = static_cast<T*>(const_cast<void*>(dout.p[e]));
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int64_t gi = int64_t(e) * g.C + c0 + v;
+      gv[v] = gam_f32 ? static_cast<const float*>(gam)[gi] : to_f32(static_cast<const bf16_t*>(gam)[gi]);
+    }
+  }
+  const int m_begin = chunk * tpb;
+  const int m_end = min(m_begin + tpb, g.M);
+  for (int m0 = m_begin; m0 < m_end; m0 += TG) {
+    float xv[TG][S][V], zv[TG][V];
+#pragma unroll
+    for (int q = 0; q < TG; ++q) {
+      const int mq = min(m0 + q, m_end - 1);  // tail: reload a valid token, add nothing
+      if constexpr (CARRIER) {
+        const int64_t p0 = cell_pixel0(mq, g, index);
+#pragma unroll
+        for (int s = 0; s < S; ++s) load_vec<T, V>(x + slot_offset<K>(p0, s, g, c0), xv[q][s]);
+      } else {
+        load_vec<T, V>(x + int64_t(mq) * g.C + c0, xv[q][0]);
+      }
+      load_vec<T, V>(ze + int64_t(mq) * g.C + c0, zv[q]);
+    }
+    load_fence();
+#pragma unroll
+    for (int q = 0; q < TG; ++q) {
+      if (m0 + q < m_end) {
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+          for (int v = 0; v < V; ++v) acc[s][v] = fmaf(xv[q][s][v], zv[q][v], acc[s][v]);
+        if constexpr (STORE_D) {
+          float d[V];
+#pragma unroll
+          for (int v = 0; v < V; ++v) d[v] = xv[q][0][v] * gv[v];
+          store_vec<T, V>(de + int64_t(m0 + q) * g.C + c0, d);
+        }
+      }
+    }
+  }
   float* prow = part + (int64_t(chunk) * E + e) * S * g.C;
 #pragma unroll
   for (int ss = 0; ss < S; ++ss) {
@@ -935,7 +1033,31 @@ int chunk_count(int64_t M, int tokens_per_chunk, int max_chunks) {
 }
 // Token chunks of the reductions: functions of sizes only, so that the workspace
 // size queries and the launches agree.
-int wgrad_chunks(int64_t M) { return chunk_count(M, SIHC_WG_CHUNK, 128); }
+// Block shape of the weight-gradient reduction: `bcg` channel-group lanes x `events`
+// event lanes (<= 256 threads), `slices` blocks across the channels.
+void wgrad_block(int C, int V, int events, int* bcg_out, int* slices_out) {
+  const int CG = (C + V - 1) / V;
+  int bcg = 64;
+  while (bcg > 1 && bcg * events > 256) bcg /= 2;
+  while (bcg > 1 && bcg / 2 >= CG) bcg /= 2;
+  *bcg_out = bcg;
+  *slices_out = (CG + bcg - 1) / bcg;
+}
+
+// Token chunks (one partial row set each) of the weight-gradient reduction: one per
+// SIHC_WG_CHUNK tokens up to 128, raised until the grid holds about 16 waves per CU
+// (few events give small blocks), with at least 32 tokens per chunk. A function of the
+// sizes only (the block shape is taken at the widest vector), so the workspace size is
+// known before the pointers are.
+int wgrad_chunks(int64_t M, int events, int C) {
+  int bcg, slices;
+  wgrad_block(C, 8, std::max(events, 1), &bcg, &slices);
+  const int64_t waves_per_chunk = int64_t(slices) * ((bcg * std::max(events, 1) + 63) / 64);
+  const int64_t want = (4096 + waves_per_chunk - 1) / waves_per_chunk;
+  const int base = chunk_count(M, SIHC_WG_CHUNK, 128);
+  const int64_t cap = std::max<int64_t>(1, std::min<int64_t>(M / 32, 2048));
+  return int(std::max<int64_t>(base, std::min(want, cap)));
+}
 int event_bwd_chunks(int64_t M) { return chunk_count(M, SIHC_EV_CHUNK, 512); }
 
 int check_geometry(const char* what, int64_t batch, int grid, int cell, int channels, Geo* g) {
@@ -1066,33 +1188,37 @@ int cells_copy(const char* what, bool gather, const void* src, const int32_t* in
   return go(uint16_t{});
 }
 
-// Shared launcher of the atomics-free weight-gradient reduction + finalize.
+// Shared launcher of the atomics-free weight-gradient reduction + finalize. With
+// `dout` (workspace mode), the update gradients dout[e] = x * gamma[e] are written in
+// the same pass.
 int launch_wgrad(const char* what, const void* x, const void* const* z, void* out, int events, const Geo& g,
                  int S, bool carrier, const int32_t* index, int dtype, int out_dtype, void* workspace,
-                 size_t workspace_bytes, hipStream_t st) {
-  const int chunks = wgrad_chunks(g.M);
+                 size_t workspace_bytes, hipStream_t st, void* const* dout = nullptr, const void* gamma = nullptr,
+                 int gamma_dtype = SIHC_DTYPE_F32) {
+  const int chunks = wgrad_chunks(g.M, events, g.C);
   const size_t need = size_t(chunks) * events * S * g.C * sizeof(float);
   if (!workspace || workspace_bytes < need)
     return fail(SIHC_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", what, need, workspace_bytes);
   if (!aligned(workspace, 16)) return fail(SIHC_ERR_INVALID, "%s: workspace must be 16-byte aligned", what);
   const int es = elem_size(dtype);
-  const void* ptrs[SIHC_MAX_EVENTS + 1];
-  for (int i = 0; i < events; ++i) ptrs[i] = z[i];
-  ptrs[events] = x;
-  const int V = pick_vec(g.C, es, 8, ptrs, events + 1);
-  const int CG = (g.C + V - 1) / V;
-  // BCG channel-group lanes x `events` event lanes <= 256 threads.
-  int bcg = 64;
-  while (bcg > 1 && bcg * events > 256) bcg /= 2;
-  while (bcg > 1 && bcg / 2 >= CG) bcg /= 2;
-  const int slices = (CG + bcg - 1) / bcg;
+  const void* ptrs[2 * SIHC_MAX_EVENTS + 1];
+  int nptr = 0;
+  for (int i = 0; i < events; ++i) ptrs[nptr++] = z[i];
+  if (dout)
+    for (int i = 0; i < events; ++i) ptrs[nptr++] = dout[i];
+  ptrs[nptr++] = x;
+  const int V = pick_vec(g.C, es, 8, ptrs, nptr);
+  int bcg, slices;
+  wgrad_block(g.C, V, events, &bcg, &slices);
   const int tpb = int((int64_t(g.M) + chunks - 1) / chunks);
   // x tile of TT tokens: at most 32 KB of LDS.
   int tt = 32768 / (S * bcg * V * int(sizeof(float)));
   tt = std::max(1, std::min(tt, 32));
   const size_t lds = size_t(tt) * S * bcg * V * sizeof(float);
   const PtrPack pk = pack(z, events);
+  const PtrPack dk = dout ? pack(const_cast<const void* const*>(dout), events) : PtrPack{};
   float* part = static_cast<float*>(workspace);
+  const int gf32 = gamma_dtype == SIHC_DTYPE_F32;
   int rc = with_dtype(dtype, [&](auto t) {
     using T = decltype(t);
     return with_vec(V, [&](auto vv) {
@@ -1100,16 +1226,27 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
       if constexpr (VV * sizeof(T) > 16) {
         return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
       } else {
-        auto go = [&](auto kk, auto car) {
+        auto go = [&](auto kk, auto car, auto sd) {
           constexpr int KK = decltype(kk)::value;
           constexpr bool CAR = decltype(car)::value;
-          hipLaunchKernelGGL((k_wgrad<T, VV, KK, CAR>), dim3(blocks1d(slices, chunks)), dim3(bcg, events), lds, st,
-                             static_cast<const T*>(x), pk, part, index, events, g, tpb, slices, tt);
+          constexpr bool SD = decltype(sd)::value;
+          if constexpr (!CAR || KK == 2) {
+            if (events <= 2) {
+              hipLaunchKernelGGL((k_wgrad_direct<T, VV, KK, CAR, SD>), dim3(blocks1d(slices, chunks)),
+                                 dim3(bcg, events), 0, st, static_cast<const T*>(x), pk, part, index, events, g,
+                                 tpb, slices, dk, gamma, gf32);
+              return check_launch(what);
+            }
+          }
+          hipLaunchKernelGGL((k_wgrad<T, VV, KK, CAR, SD>), dim3(blocks1d(slices, chunks)), dim3(bcg, events), lds,
+                             st, static_cast<const T*>(x), pk, part, index, events, g, tpb, slices, tt, dk, gamma,
+                             gf32);
           return check_launch(what);
         };
-        if (!carrier) return go(IC<2>{}, std::false_type{});
-        if (g.K == 2) return go(IC<2>{}, std::true_type{});
-        return go(IC<4>{}, std::true_type{});
+        if (!carrier && dout) return go(IC<2>{}, std::false_type{}, std::true_type{});
+        if (!carrier) return go(IC<2>{}, std::false_type{}, std::false_type{});
+        if (g.K == 2) return go(IC<2>{}, std::true_type{}, std::false_type{});
+        return go(IC<4>{}, std::true_type{}, std::false_type{});
       }
     });
   });
@@ -1230,7 +1367,7 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
 size_t sihc_weight_grad_workspace_size(int events, int64_t batch, int grid, int cell, int channels) {
   if (events < 1 || batch < 0 || grid <= 0 || cell <= 0 || channels <= 0) return 0;
   const int64_t M = batch * int64_t(grid) * grid;
-  return size_t(wgrad_chunks(M)) * events * cell * cell * channels * sizeof(float);
+  return size_t(wgrad_chunks(M, events, channels)) * events * cell * cell * channels * sizeof(float);
 }
 
 int sihc_weight_grad(const void* x, const void* const* z, void* out, int events, int64_t batch, int grid, int cell,
@@ -1294,7 +1431,7 @@ int sihc_triangular(const void* base, const void* const* updates, const void* ga
 
 size_t sihc_triangular_gamma_grad_workspace_size(int active, int64_t rows, int channels) {
   if (active < 1 || rows < 0 || channels <= 0) return 0;
-  return size_t(wgrad_chunks(rows)) * active * channels * sizeof(float);
+  return size_t(wgrad_chunks(rows, active, channels)) * active * channels * sizeof(float);
 }
 
 int sihc_triangular_gamma_grad(const void* grad, const void* const* updates, void* out, int active, int64_t rows,
@@ -1318,6 +1455,32 @@ int sihc_triangular_gamma_grad(const void* grad, const void* const* updates, voi
   g.C = channels;
   return launch_wgrad(what, grad, updates, out, active, g, 1, false, nullptr, dtype, out_dtype, workspace,
                       workspace_bytes, st);
+}
+
+int sihc_triangular_backward(const void* grad, const void* const* updates, const void* gamma,
+                             void* const* grad_updates, void* grad_gamma, int active, int64_t rows, int channels,
+                             int dtype, int gamma_dtype, int out_dtype, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  const char* what = "sihc_triangular_backward";
+  if (rows < 0 || rows >= (int64_t(1) << 31) || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
+  if (!valid_dtype(dtype) || !valid_dtype(gamma_dtype) || !valid_dtype(out_dtype))
+    return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
+  if (int rc = check_count(what, active)) return rc;
+  if (!grad_gamma || !grad_updates) return fail(SIHC_ERR_INVALID, "%s: null output", what);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (rows == 0) return fill_zero(out_dtype, grad_gamma, int64_t(active) * channels, st, what);
+  if (!grad || !gamma) return fail(SIHC_ERR_INVALID, "%s: null input", what);
+  if (int rc = check_events(what, active, updates)) return rc;
+  if (int rc = check_events(what, active, const_cast<const void* const*>(grad_updates))) return rc;
+  Geo g;
+  g.M = int(rows);
+  g.GG = 1;
+  g.G = 1;
+  g.K = 1;
+  g.GK = 1;
+  g.C = channels;
+  return launch_wgrad(what, grad, updates, grad_gamma, active, g, 1, false, nullptr, dtype, out_dtype, workspace,
+                      workspace_bytes, st, grad_updates, gamma, gamma_dtype);
 }
 
 int sihc_event_forward(const void* x, const void* dz, const void* beta, const void* alpha_next, void* x_out,

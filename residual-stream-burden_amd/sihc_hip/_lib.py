@@ -32,6 +32,8 @@ PROTOTYPES: dict[str, tuple] = {
     "sihc_triangular": (_i32, [_vp, _vpp, _vp, _vp, _i32, _i64, _i32, _i32, _i32, _vp]),
     "sihc_triangular_gamma_grad_workspace_size": (_sz, [_i32, _i64, _i32]),
     "sihc_triangular_gamma_grad": (_i32, [_vp, _vpp, _vp, _i32, _i64, _i32, _i32, _i32, _vp, _sz, _vp]),
+    "sihc_triangular_backward": (_i32, [_vp, _vpp, _vp, _vpp, _vp, _i32, _i64, _i32, _i32, _i32, _i32,
+                                        _vp, _sz, _vp]),
     "sihc_event_forward": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _vp, _i32, _vp]),
     "sihc_event_backward_workspace_size": (_sz, [_i64, _i32, _i32, _i32]),
     "sihc_event_backward": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,

@@ -47,11 +47,14 @@ def carrier_geometry(x: Tensor, slots: int) -> tuple[int, int, int, int]:
     return b, h // k, k, c
 
 
-def read(x: Tensor, alpha: Tensor, index: Optional[Tensor] = None) -> list[Tensor]:
-    """E base reads of carrier x [B,H,W,C] with stacked alpha [E,C,S]."""
+def read(x: Tensor, alpha: Tensor, index: Optional[Tensor] = None,
+         out: Optional[Sequence[Tensor]] = None) -> list[Tensor]:
+    """E base reads of carrier x [B,H,W,C] with stacked alpha [E,C,S] (into `out` if given)."""
     b, g, k, c = carrier_geometry(x, alpha.shape[2])
     events = alpha.shape[0]
-    out = [torch.empty((b, g * g, c), device=x.device, dtype=x.dtype) for _ in range(events)]
+    if out is None:
+        out = [torch.empty((b, g * g, c), device=x.device, dtype=x.dtype) for _ in range(events)]
+    out = list(out)
     check(lib().sihc_read(x.data_ptr(), alpha.data_ptr(), ptr_array(o.data_ptr() for o in out), events,
                           b, g, k, c, _ptr(index), dtype_code(x.dtype), _stream(x.device)))
     return out
@@ -69,17 +72,22 @@ def write(x: Tensor, updates: Sequence[Tensor], beta: Tensor, add_x: bool = True
     return out
 
 
-def weight_grad(x: Tensor, updates: Sequence[Tensor], weights: Tensor,
-                index: Optional[Tensor] = None) -> Tensor:
-    """[E,C,S] (weights dtype) = sum over tokens of x[m,s,c] * updates_e[m,c]."""
-    b, g, k, c = carrier_geometry(x, weights.shape[2])
+def weight_grad(x: Tensor, updates: Sequence[Tensor], weights: Optional[Tensor],
+                index: Optional[Tensor] = None, out_dtype: Optional[torch.dtype] = None,
+                slots: Optional[int] = None) -> Tensor:
+    """[E,C,S] = sum over tokens of x[m,s,c] * updates_e[m,c], reduced in fp32.
+
+    Stored in out_dtype (default: the weights' dtype); `slots` and `out_dtype` stand in
+    for `weights` when there is no weight tensor at hand.
+    """
+    b, g, k, c = carrier_geometry(x, slots if weights is None else weights.shape[-1])
     events = len(updates)
-    out = torch.empty((events, c, k * k), device=x.device, dtype=weights.dtype)
+    out = torch.empty((events, c, k * k), device=x.device, dtype=out_dtype or weights.dtype)
     L = lib()
     nbytes = L.sihc_weight_grad_workspace_size(events, b, g, k, c)
     ws = _workspace(nbytes, x.device)
     check(L.sihc_weight_grad(x.data_ptr(), ptr_array(u.data_ptr() for u in updates), out.data_ptr(), events,
-                             b, g, k, c, _ptr(index), dtype_code(x.dtype), dtype_code(weights.dtype),
+                             b, g, k, c, _ptr(index), dtype_code(x.dtype), dtype_code(out.dtype),
                              ws.data_ptr(), ws.numel() * 4, _stream(x.device)))
     return out
 
@@ -95,19 +103,41 @@ def triangular(base: Tensor, updates: Sequence[Tensor], gamma: Tensor) -> Tensor
     return out
 
 
-def triangular_gamma_grad(grad: Tensor, updates: Sequence[Tensor], gamma: Tensor) -> Tensor:
-    """[A,C] (gamma dtype) = sum over rows of grad * updates_j."""
+def triangular_gamma_grad(grad: Tensor, updates: Sequence[Tensor], gamma: Optional[Tensor],
+                          out_dtype: Optional[torch.dtype] = None) -> Tensor:
+    """[A,C] (out_dtype, default gamma's dtype) = sum over rows of grad * updates_j."""
     c = grad.shape[-1]
     rows = grad.numel() // c if c else 0
     active = len(updates)
-    out = torch.empty((active, c), device=grad.device, dtype=gamma.dtype)
+    out = torch.empty((active, c), device=grad.device, dtype=out_dtype or gamma.dtype)
     L = lib()
     ws = _workspace(L.sihc_triangular_gamma_grad_workspace_size(active, rows, c), grad.device)
     check(L.sihc_triangular_gamma_grad(grad.data_ptr(), ptr_array(u.data_ptr() for u in updates),
                                        out.data_ptr(), active, rows, c, dtype_code(grad.dtype),
-                                       dtype_code(gamma.dtype), ws.data_ptr(), ws.numel() * 4,
+                                       dtype_code(out.dtype), ws.data_ptr(), ws.numel() * 4,
                                        _stream(grad.device)))
     return out
+
+
+def triangular_backward(grad: Tensor, updates: Sequence[Tensor], gamma: Tensor,
+                        out_dtype: Optional[torch.dtype] = None) -> tuple[Tensor, Tensor]:
+    """One pass: ([A,B,N,C] stack of grad * gamma[j], [A,C] sum over rows of grad * updates_j).
+
+    The update gradients share grad's dtype; the gamma gradient is out_dtype (default
+    gamma's dtype), reduced in fp32.
+    """
+    c = grad.shape[-1]
+    rows = grad.numel() // c if c else 0
+    active = len(updates)
+    ddz = torch.empty((active, *grad.shape), device=grad.device, dtype=grad.dtype)
+    dg = torch.empty((active, c), device=grad.device, dtype=out_dtype or gamma.dtype)
+    L = lib()
+    ws = _workspace(L.sihc_triangular_gamma_grad_workspace_size(active, rows, c), grad.device)
+    check(L.sihc_triangular_backward(grad.data_ptr(), ptr_array(u.data_ptr() for u in updates), gamma.data_ptr(),
+                                     ptr_array(d.data_ptr() for d in ddz.unbind(0)), dg.data_ptr(), active, rows,
+                                     c, dtype_code(grad.dtype), dtype_code(gamma.dtype), dtype_code(dg.dtype),
+                                     ws.data_ptr(), ws.numel() * 4, _stream(grad.device)))
+    return ddz, dg
 
 
 def event_forward(x: Tensor, dz: Tensor, beta: Tensor, alpha_next: Optional[Tensor],
@@ -185,5 +215,6 @@ def copy_(dst: Tensor, src: Tensor) -> Tensor:
 
 __all__ = [
     "MAX_EVENTS", "dtype_code", "carrier_geometry", "read", "write", "weight_grad", "triangular",
-    "triangular_gamma_grad", "event_forward", "event_backward", "gather_cells", "scatter_cells", "copy_",
+    "triangular_gamma_grad", "triangular_backward", "event_forward", "event_backward", "gather_cells",
+    "scatter_cells", "copy_",
 ]

@@ -166,19 +166,28 @@ def _tri_gamma_backward(grad: Tensor, updates: list[Tensor], gamma: Tensor) -> T
     return launch.triangular_gamma_grad(grad, updates, gamma)
 
 
+@custom_op("sihc::sublayer_triangular_backward", mutates_args=())
+def _tri_backward(grad: Tensor, updates: list[Tensor], gamma: Tensor) -> tuple[Tensor, Tensor]:
+    """([A,B,N,C] update gradients grad * gamma_j, dgamma) from one pass over grad.
+
+    Same values as the reference's backward (:369-379: fp32 products cast to the
+    workspace dtype, and `_tri_gamma_backward`), with grad read once instead of A + 1
+    times.
+    """
+    return launch.triangular_backward(grad, updates, gamma)
+
+
 def _tri_setup(ctx, inputs, output):
     _, updates, gamma = inputs
     ctx.save_for_backward(gamma, *updates)
 
 
 def _tri_autograd(ctx, grad):
-    """Reference :369-379: the update gradients stay ordinary (fusable) elementwise
-    tensor ops, fp32 product then cast to the workspace dtype."""
+    """Reference :369-379: identity to base, grad * gamma_j to each active update and
+    the gamma reduction, all from `_tri_backward`."""
     gamma, *updates = ctx.saved_tensors
-    grad = grad.contiguous()
-    dg = _tri_gamma_backward(grad, updates, gamma)
-    ddz = [(grad.float() * gamma[i].float()).to(grad.dtype) for i in range(len(updates))]
-    return grad, ddz, dg
+    ddz, dg = _tri_backward(grad.contiguous(), updates, gamma)
+    return grad, list(ddz.unbind(0)), dg
 
 
 register_autograd(sublayer_triangular, _tri_autograd, setup_context=_tri_setup)
@@ -225,5 +234,10 @@ def _tri_gamma_backward_fake(grad, updates, gamma):
     return torch.empty_like(gamma)
 
 
+@_tri_backward.register_fake
+def _tri_backward_fake(grad, updates, gamma):
+    return grad.new_empty((len(updates), *grad.shape)), torch.empty_like(gamma)
+
+
 __all__ = ["sublayer_read", "sublayer_write", "sublayer_triangular", "_write_impl",
-           "_weights_backward", "_tri_gamma_backward", "_require_packed", "_geometry"]
+           "_weights_backward", "_tri_gamma_backward", "_tri_backward", "_require_packed", "_geometry"]

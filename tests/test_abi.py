@@ -35,7 +35,9 @@ def test_workspace_sizes_are_pure_functions_of_sizes():
     ws = lib.sihc_weight_grad_workspace_size(24, 256, 16, 2, 1152)
     assert ws == 128 * 24 * 4 * 1152 * 4
     assert lib.sihc_weight_grad_workspace_size(0, 256, 16, 2, 1152) == 0
-    assert lib.sihc_triangular_gamma_grad_workspace_size(3, 147, 67) == 1 * 3 * 67 * 4
+    # few event lanes: more chunks (about 16 waves per CU), at least 32 tokens each
+    assert lib.sihc_triangular_gamma_grad_workspace_size(3, 147, 67) == 4 * 3 * 67 * 4
+    assert lib.sihc_triangular_gamma_grad_workspace_size(1, 65536, 1152) == 1366 * 1 * 1152 * 4
     assert lib.sihc_event_backward_workspace_size(256, 16, 2, 1152) == 256 * 2 * 4 * 1152 * 4
 
 
@@ -77,6 +79,23 @@ def test_too_small_workspace_is_rejected():
     rc = lib.sihc_event_backward(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
                                  256, 16, 2, 1152, None, 1, 1, FAKE, 16, None)
     assert rc == 1 and b"workspace of" in lib.sihc_last_error()
+    rc = lib.sihc_triangular_backward(FAKE, ups, FAKE, ups, FAKE, 1, 65536, 1152, 1, 1, 0, FAKE, 16, None)
+    assert rc == 1 and b"workspace of" in lib.sihc_last_error()
+
+
+def test_triangular_backward_arguments_are_validated():
+    lib = _lib.lib()
+    ups = _lib.ptr_array([FAKE, FAKE])
+    nulls = _lib.ptr_array([FAKE, None])
+    ws = 1 << 30
+    assert lib.sihc_triangular_backward(FAKE, ups, FAKE, nulls, FAKE, 2, 512, 64, 1, 1, 0, FAKE, ws, None) == 1
+    assert b"null tensor pointer 1" in lib.sihc_last_error()
+    assert lib.sihc_triangular_backward(FAKE, ups, FAKE, ups, None, 2, 512, 64, 1, 1, 0, FAKE, ws, None) == 1
+    assert b"null output" in lib.sihc_last_error()
+    assert lib.sihc_triangular_backward(FAKE, ups, FAKE, ups, FAKE, 2, 512, 64, 1, 5, 0, FAKE, ws, None) == 1
+    assert b"bad dtype" in lib.sihc_last_error()
+    assert lib.sihc_triangular_backward(FAKE, ups, FAKE, ups, FAKE, 33, 512, 64, 1, 1, 0, FAKE, ws, None) == 1
+    assert b"1..32" in lib.sihc_last_error()
 
 
 def test_oversized_tensor_is_rejected():

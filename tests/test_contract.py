@@ -2,7 +2,8 @@
 
 Every check here raises before any device work, so it runs without a GPU
 (the reference's checks, sihc/models/sihc/sublayer_kernels.py:180-193, 235-243,
-337-347, and the packed-layout test research/tests/test_sublayer_kernels.py:111-121).
+337-347, kernels.py:1770, 1792-1801, 2224-2227, 2345-2350, 2439-2442, 2536, and the
+packed-layout test research/tests/test_sublayer_kernels.py:111-121).
 """
 from __future__ import annotations
 
@@ -12,6 +13,7 @@ import torch
 from sihc_hip import blockwise_kernels as BK
 from sihc_hip import event_ops as EV
 from sihc_hip import indexed as IX
+from sihc_hip import kernels as LK
 from sihc_hip import sublayer_kernels as SK
 
 
@@ -96,3 +98,43 @@ def test_index_contract():
         IX.check_index(idx.long(), 3, 4, permutation=False)
     # seeded: same seed, same assignment
     assert torch.equal(idx, IX.group_index(3, grid=4, group=5, seed=1))
+
+
+def test_legacy_op_surface_and_shape_checks():
+    # every reference op name is registered, one triangular op per prefix length
+    assert len(LK.triangular_accumulate_b4_12_ptr_active_traceable_ops) == 11
+    assert len(LK.triangular_accumulate_b4_8_ptr_active_traceable_ops) == 7
+    for name in ("all_base_b4_12_split_traceable", "all_base_b4_8_split_traceable", "all_base_p8_12_split_traceable",
+                 "all_base_b4_12_grad_x", "all_base_p8_12_split_grad_alpha", "final_accumulate_b4_12_traceable",
+                 "final_accumulate_p8_12_grad_dz_ptr", "final_accumulate_b4_8_grad_beta_ptr",
+                 "triangular_accumulate_b4_12_ptr_active11", "triangular_accumulate_b4_8_ptr_active7_grad_fused",
+                 "triangular_accumulate_b4_12_ptr_active3_grad_gamma", "cell_mean_b4_traceable",
+                 "cell_mean_b4_backward_traceable"):
+        assert hasattr(torch.ops.sihc, name), name
+    schema = str(torch.ops.sihc.final_accumulate_b4_12_traceable.default._schema)
+    assert "Tensor dz11" in schema and "Tensor beta11" in schema
+    with pytest.raises(ValueError, match=r"active must be in \[1, 11\]"):
+        LK._make_triangular(12, 12)
+    with pytest.raises(ValueError, match=r"all_base_b4_12_split expects x0 \[B,64,64,C\] and alpha \[12,C,16\]"):
+        LK.all_base_b4_12_split_traceable(torch.randn(1, 32, 32, 8), torch.randn(12, 8, 16))
+    with pytest.raises(ValueError, match=r"all_base_p8_12_split expects x0 \[B,32,32,C\] and alpha \[12,C,4\]"):
+        LK.all_base_p8_12_split_traceable(torch.randn(1, 32, 32, 8), torch.randn(8, 8, 4))
+    with pytest.raises(ValueError, match="CUDA device"):
+        LK.all_base_b4_8_split_traceable(torch.randn(1, 64, 64, 8), torch.randn(8, 8, 16))
+    with pytest.raises(ValueError, match=r"final_accumulate_p8_12 expects x0 \[B,32,32,C\]"):
+        LK.final_accumulate_p8_12_traceable(torch.randn(1, 64, 64, 8), *[torch.randn(1, 256, 8)] * 12,
+                                            *[torch.randn(8, 4)] * 12)
+    with pytest.raises(ValueError, match="beta3 must be"):
+        betas = [torch.randn(8, 16)] * 8
+        betas[3] = torch.randn(8, 4)
+        LK.final_accumulate_b4_8_traceable(torch.randn(1, 64, 64, 8), *[torch.randn(1, 256, 8)] * 8, *betas)
+    base = torch.randn(1, 256, 8)
+    ops = LK.triangular_accumulate_b4_12_ptr_active_traceable_ops
+    with pytest.raises(ValueError, match=r"expects base \[B,256,C\] and gamma \[12,C\]"):
+        ops[0](base, *[base] * 12, torch.randn(11, 8))
+    with pytest.raises(ValueError, match="dz4 shape"):
+        dzs = [base] * 12
+        dzs[4] = torch.randn(1, 255, 8)
+        ops[2](base, *dzs, torch.randn(12, 8))
+    with pytest.raises(ValueError, match=r"cell_mean_b4 expects x \[B,64,64,C\]"):
+        LK.cell_mean_b4_traceable(torch.randn(1, 32, 32, 8))

@@ -128,6 +128,35 @@ def test_weight_gradients_match_autograd():
     torch.testing.assert_close(O.triangular_gamma_grad(go, ups).double(), dg, rtol=1e-6, atol=1e-6)
 
 
+def test_triangular_backward_matches_autograd():
+    torch.manual_seed(5)
+    base = torch.randn(2, 16, 3, dtype=torch.float64, requires_grad=True)
+    ups = [torch.randn(2, 16, 3, dtype=torch.float64, requires_grad=True) for _ in range(4)]
+    gamma = torch.randn(4, 3, dtype=torch.float64, requires_grad=True)
+    go = torch.randn(2, 16, 3, dtype=torch.float64)
+    grads = torch.autograd.grad((O.triangular_torch(base, ups, gamma) * go).sum(), (base, *ups, gamma))
+    torch.testing.assert_close(grads[0], go)
+    ddz, dg = O.triangular_backward(go, [u.detach() for u in ups], gamma.detach())
+    for a, b in zip(ddz, grads[1:5]):
+        torch.testing.assert_close(a, b)
+    torch.testing.assert_close(dg.double(), grads[5], rtol=1e-6, atol=1e-6)
+
+
+def test_cell_mean_is_average_pooling_over_cells():
+    # Pinned by torch's 4x4 average pooling of the NCHW carrier: a wrong cell map (rows
+    # and columns swapped, a 2x2 cell) or a wrong scale fails it.
+    torch.manual_seed(6)
+    x = torch.randn(2, 64, 64, 5, dtype=torch.float64)
+    pooled = torch.nn.functional.avg_pool2d(x.permute(0, 3, 1, 2), 4)         # [B,C,16,16]
+    expected = pooled.permute(0, 2, 3, 1).reshape(2, 256, 5)
+    torch.testing.assert_close(O.cell_mean(x), expected)
+    # fp32: the fp32 slot-order sum times 1/16 (exact scaling) equals the fp64 mean
+    # rounded once only up to the sum's rounding
+    x32 = x.float()
+    torch.testing.assert_close(O.cell_mean(x32).double(), expected, rtol=1e-6, atol=1e-6)
+    assert O.cell_mean(x32.bfloat16()).dtype == torch.bfloat16
+
+
 def test_event_backward_matches_autograd():
     torch.manual_seed(3)
     x = torch.randn(2, 6, 6, 4, dtype=torch.float64, requires_grad=True)
