@@ -53,6 +53,8 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--schedule", choices=("stage", "literal"), default="stage",
                    help="routing schedule of --mode e2e")
+    p.add_argument("--slots", type=int, choices=(4, 16), default=4,
+                   help="cell slots of --mode kernels: 4 (p8, 32x32 carrier) or 16 (p4, 64x64 carrier)")
     p.add_argument("--mode", choices=("step", "calibrate", "kernels", "e2e"), default="step",
                    help="step: the benchmark (default); calibrate: a 1 GiB copy-kernel launch plus single "
                         "event forward/backward launches at the same shape, for HBM counter runs; kernels: "
@@ -228,8 +230,42 @@ def extra_configs(seed: int) -> dict:
     }
     del xs, dz, x0
     torch.cuda.empty_cache()
+    # ---- 16-slot cells (patch 4, 64x64 carrier): the same 24-event forward at D=1152
+    B, C, E, S = 256, 1152, 24, 16
+    U = B * 256 * C * ELEM
+    x0 = r((B, 64, 64, C))
+    alpha = r((E, C, S), 1.0 / S, 0.02)
+    beta = r((E, C, S), 1.0, 0.02)
+    dz = [r((B, 256, C)) for _ in range(E)]
+    gamma = (alpha[:, None].float() * beta[None, :].float()).sum(-1).to(bf)
+    xs = [x0, torch.empty_like(x0), torch.empty_like(x0)]
+
+    def literal16():
+        launch.read(x0, alpha[:1])
+        for i in range(E):
+            src = x0 if i == 0 else xs[1 + (i - 1) % 2]
+            launch.event_forward(src, dz[i], beta[i], alpha[i + 1] if i + 1 < E else None)
+
+    def stage16():
+        base = launch.read(x0, alpha)
+        for i in range(1, E):
+            launch.triangular(base[i], dz[:i], gamma[i, :i].contiguous())
+        launch.write(x0, dz, beta)
+
+    lit_bytes = ((S + 1) + (E - 1) * (2 * S + 2) + (2 * S + 1)) * U
+    stage_bytes = ((S + E) + sum(i + 2 for i in range(1, E)) + (2 * S + E)) * U
+    t_lit, t_stage = _timed(torch, literal16, iters=3), _timed(torch, stage16, iters=3)
+    out["p4_forward"] = {
+        "workload": "16-slot cells: batch 256, 64x64 carrier, D=1152, 24 events, forward only, bf16",
+        "per_event_fused": {"ms": round(t_lit * 1e3, 3), "GB/s": round(lit_bytes / t_lit / 1e9, 1),
+                            "bytes": lit_bytes, "tokens_per_s": round(B * 256 / t_lit, 1)},
+        "stage_api": {"ms": round(t_stage * 1e3, 3), "GB/s": round(stage_bytes / t_stage / 1e9, 1),
+                      "bytes": stage_bytes, "tokens_per_s": round(B * 256 / t_stage, 1)},
+    }
+    del xs, dz, x0
+    torch.cuda.empty_cache()
     # ---- config 3
-    B, C = 128, 1152
+    B, C, S = 128, 1152, 4
     U = B * 256 * C * ELEM
     x = r((B, 32, 32, C))
     idx = group_index(B, 16, 5, seed=3).to(dev)
@@ -358,12 +394,13 @@ def kernels(args) -> None:
 
     dev = torch.device("cuda", 0)
     bf = torch.bfloat16
-    B, C, S = args.batch, args.channels, 4
+    B, C, S = args.batch, args.channels, args.slots
+    edge = 32 if S == 4 else 64
     g = torch.Generator(device=dev).manual_seed(args.seed)
     r = lambda shape, m=0.0, sd=1.0: (m + sd * torch.randn(shape, device=dev, generator=g)).to(bf)  # noqa: E731
-    x = r((B, 32, 32, C))
+    x = r((B, edge, edge, C))
     ws = [r((B, 256, C)) for _ in range(25)]
-    alpha = r((24, C, S), 0.25, 0.02)
+    alpha = r((24, C, S), 1.0 / S, 0.02)
     beta = r((24, C, S), 1.0, 0.02)
     gamma = (0.05 * torch.randn(24, C, device=dev, generator=g))
     U = B * 256 * C * ELEM
@@ -396,9 +433,9 @@ def kernels(args) -> None:
     for a in (1, 11, 23):
         cases.append((f"triangular_backward A={a}", (2 * a + 1) * U,
                       lambda a=a: launch.triangular_backward(ws[24], ws[:a], gamma[:a])))
-    cases.append(("event_forward", 10 * U, lambda: launch.event_forward(x, ws[0], beta[0], alpha[1])))
-    h = r((B, 32, 32, C), 0.0, 1e-2)
-    cases.append(("event_backward", 15 * U,
+    cases.append(("event_forward", (2 * S + 2) * U, lambda: launch.event_forward(x, ws[0], beta[0], alpha[1])))
+    h = r((B, edge, edge, C), 0.0, 1e-2)
+    cases.append(("event_backward", (3 * S + 3) * U,
                   lambda: launch.event_backward(h, ws[1], x, ws[0], beta[0], alpha[1])))
     cp_src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     cp_dst = torch.empty_like(cp_src)

@@ -60,6 +60,21 @@
 #ifndef SIHC_RW_TPT  // tokens per lane, read / write / triangular
 #define SIHC_RW_TPT 8
 #endif
+// 16-slot cells: a lane holds 16 slot vectors per token and reads 16 weights per event
+// and channel from LDS, so read / write use narrow vectors and 2 tokens per lane (wider
+// shapes exceed 256 VGPRs), and a smaller LDS budget per block keeps 3+ blocks per CU.
+#ifndef SIHC_RW_UNROLL_K4  // tokens per lane per iteration of k_read / k_write, 16 slots
+#define SIHC_RW_UNROLL_K4 2
+#endif
+#ifndef SIHC_RW_VEC_K4  // widest vector of k_read / k_write, 16 slots
+#define SIHC_RW_VEC_K4 2
+#endif
+#ifndef SIHC_RW_BCG_K4  // channel-group lanes per block of k_read / k_write, 16 slots
+#define SIHC_RW_BCG_K4 32
+#endif
+#ifndef SIHC_RW_LDS_K4  // LDS bytes per block for staged weights, 16 slots
+#define SIHC_RW_LDS_K4 (48 * 1024)
+#endif
 #ifndef SIHC_WG_CHUNK  // tokens per reduction chunk, weight / gamma gradients
 #define SIHC_WG_CHUNK 512
 #endif
@@ -266,7 +281,8 @@ __global__ void __launch_bounds__(256) k_read(const T* __restrict__ x, const T* 
                                               PtrPack out, const int32_t* __restrict__ index,
                                               int E, Geo g, int tpb, int nslices) {
   constexpr int S = K * K;
-  constexpr int U = SIHC_RW_UNROLL;  // tokens per lane per iteration: each LDS weight feeds U tokens
+  // tokens per lane per iteration: each LDS weight feeds U tokens
+  constexpr int U = K == 2 ? SIHC_RW_UNROLL : SIHC_RW_UNROLL_K4;
   extern __shared__ float lds[];
   const int BCG = blockDim.x, TL = blockDim.y;
   const int BC = BCG * V;
@@ -324,7 +340,8 @@ __global__ void __launch_bounds__(256) k_write(const TX* __restrict__ x, PtrPack
                                                const int32_t* __restrict__ index, int E, Geo g, int tpb,
                                                int nslices) {
   constexpr int S = K * K;
-  constexpr int U = SIHC_RW_UNROLL;  // tokens per lane per iteration: each LDS weight feeds U tokens
+  // tokens per lane per iteration: each LDS weight feeds U tokens
+  constexpr int U = K == 2 ? SIHC_RW_UNROLL : SIHC_RW_UNROLL_K4;
   constexpr int EG = U > 1 ? 2 : 4;  // events per load group
   extern __shared__ float lds[];
   const int BCG = blockDim.x, TL = blockDim.y;
@@ -616,6 +633,135 @@ __global__ void __launch_bounds__(256) k_wgrad_direct(const T* __restrict__ x, P
   for (int ss = 0; ss < S; ++ss) {
 #pragma unroll
     for (int v = 0; v < V; ++v) prow[int64_t(ss) * g.C + c0 + v] = acc[ss][v];
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// Weight gradient of 16-slot cells (K = 4). k_wgrad's lane (event, channel group)
+// would hold 16 x V accumulators and re-read the 16 staged slot values per token for
+// every event lane. Here a lane owns ONE channel and a group of C16_EPL events: its
+// 16 x C16_EPL accumulators live in registers and every carrier value staged in LDS
+// feeds C16_EPL FMAs. Blocks are C16_LANES channel lanes x event groups; the carrier
+// tile is staged in LDS once per block, with 16-byte global loads.
+// ----------------------------------------------------------------------------------
+constexpr int C16_LANES = 64;  // channels per block slice (one per lane of a wave)
+constexpr int C16_EPL = 4;     // events per lane
+#ifndef SIHC_C16_NQ  // staging loads in flight per thread
+#define SIHC_C16_NQ 2
+#endif
+
+// LDS carrier tile of 16-slot cells: xt[(t*16 + s)*64 + cl] = x[token t0+t, slot s,
+// channel cs+cl], t < tn, raw element copies in VS-element vectors.
+template <typename T, int VS>
+__device__ __forceinline__ void stage_cells16(T* __restrict__ xt, const T* __restrict__ x, int t0, int tn, int cs,
+                                              const Geo& g, const int32_t* __restrict__ index) {
+  constexpr int NV = C16_LANES / VS;
+  constexpr int NQ = SIHC_C16_NQ;
+  using R = typename RawT<VS * int(sizeof(T))>::type;
+  const int tid = threadIdx.y * blockDim.x + threadIdx.x;
+  const int nthr = blockDim.x * blockDim.y;
+  const int total = tn * 16 * NV;
+  for (int i0 = tid; i0 < total; i0 += NQ * nthr) {
+    R v[NQ];
+    int dst[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int i = i0 + q * nthr;
+      dst[q] = -1;
+      if (i < total) {
+        const int row = i / NV, j = i - row * NV;
+        const int c = cs + j * VS;
+        if (c < g.C) {
+          const int64_t off = slot_offset<4>(cell_pixel0(t0 + (row >> 4), g, index), row & 15, g, c);
+          v[q] = *reinterpret_cast<const R*>(x + off);
+          dst[q] = row * C16_LANES + j * VS;
+        }
+      }
+    }
+    load_fence();
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+      if (dst[q] >= 0) *reinterpret_cast<R*>(xt + dst[q]) = v[q];
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void stage_cells16_any(int vs, T* xt, const T* x, int t0, int tn, int cs, const Geo& g,
+                                                  const int32_t* index) {
+  if (vs * int(sizeof(T)) == 16) {
+    stage_cells16<T, 16 / int(sizeof(T))>(xt, x, t0, tn, cs, g, index);
+  } else if (vs * int(sizeof(T)) == 8) {
+    stage_cells16<T, 8 / int(sizeof(T))>(xt, x, t0, tn, cs, g, index);
+  } else if (vs * int(sizeof(T)) == 4) {
+    stage_cells16<T, 4 / int(sizeof(T))>(xt, x, t0, tn, cs, g, index);
+  } else {
+    stage_cells16<T, 1>(xt, x, t0, tn, cs, g, index);
+  }
+}
+
+// weight gradient, 16 slots: lane (channel c, event group eg) accumulates
+// part[chunk][e][s][c] = sum_{m in chunk} x[m,s,c] * z_e[m,c] for its 4 events in
+// registers, tokens in ascending order (the same partial rows as k_wgrad).
+template <typename T>
+__global__ void __launch_bounds__(512) k_wgrad16(const T* __restrict__ x, PtrPack z, float* __restrict__ part,
+                                                 const int32_t* __restrict__ index, int E, Geo g, int tpb,
+                                                 int nslices, int vs) {
+  constexpr int S = 16;
+  constexpr int TT = 32 / int(sizeof(T));
+  constexpr int TG = 4;  // tokens whose update loads are issued together
+  __shared__ T xt[TT * S * C16_LANES];
+  const int lane = threadIdx.x;
+  const int e0 = __builtin_amdgcn_readfirstlane(threadIdx.y) * C16_EPL;
+  const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
+  const int cs = slice * C16_LANES, c = cs + lane;
+  const bool cok = c < g.C;
+  const T* ze[C16_EPL];
+#pragma unroll
+  for (int q = 0; q < C16_EPL; ++q) ze[q] = static_cast<const T*>(z.p[min(e0 + q, E - 1)]);
+  float acc[C16_EPL][S];
+#pragma unroll
+  for (int q = 0; q < C16_EPL; ++q)
+#pragma unroll
+    for (int s = 0; s < S; ++s) acc[q][s] = 0.f;
+  const int m_begin = chunk * tpb;
+  const int m_end = min(m_begin + tpb, g.M);
+  for (int t0 = m_begin; t0 < m_end; t0 += TT) {
+    const int tn = min(TT, m_end - t0);
+    stage_cells16_any<T>(vs, xt, x, t0, tn, cs, g, index);
+    __syncthreads();
+    if (cok) {
+      for (int t = 0; t < tn; t += TG) {
+        float zv[TG][C16_EPL];
+#pragma unroll
+        for (int u = 0; u < TG; ++u) {
+          const int64_t zoff = int64_t(t0 + min(t + u, tn - 1)) * g.C + c;  // clamp: reloaded, not added
+#pragma unroll
+          for (int q = 0; q < C16_EPL; ++q) zv[u][q] = to_f32(ze[q][zoff]);
+        }
+        load_fence();
+#pragma unroll
+        for (int u = 0; u < TG; ++u) {
+          if (t + u < tn) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+              const float xs = to_f32(xt[((t + u) * S + s) * C16_LANES + lane]);
+#pragma unroll
+              for (int q = 0; q < C16_EPL; ++q) acc[q][s] = fmaf(xs, zv[u][q], acc[q][s]);
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (!cok) return;
+#pragma unroll
+  for (int q = 0; q < C16_EPL; ++q) {
+    if (e0 + q < E) {
+      float* prow = part + (int64_t(chunk) * E + e0 + q) * S * g.C + c;
+#pragma unroll
+      for (int s = 0; s < S; ++s) prow[int64_t(s) * g.C] = acc[q][s];
+    }
   }
 }
 
@@ -1217,6 +1363,9 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
   const size_t lds = size_t(tt) * S * bcg * V * sizeof(float);
   const PtrPack pk = pack(z, events);
   const PtrPack dk = dout ? pack(const_cast<const void* const*>(dout), events) : PtrPack{};
+  // 16-slot carrier: k_wgrad16 (one channel per lane); only x is loaded as vectors
+  const int slices16 = (g.C + C16_LANES - 1) / C16_LANES;
+  const int vs16 = pick_vec(g.C, es, 8, &x, 1);
   float* part = static_cast<float*>(workspace);
   const int gf32 = gamma_dtype == SIHC_DTYPE_F32;
   int rc = with_dtype(dtype, [&](auto t) {
@@ -1230,17 +1379,21 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
           constexpr int KK = decltype(kk)::value;
           constexpr bool CAR = decltype(car)::value;
           constexpr bool SD = decltype(sd)::value;
-          if constexpr (!CAR || KK == 2) {
+          if constexpr (CAR && KK == 4) {
+            hipLaunchKernelGGL((k_wgrad16<T>), dim3(blocks1d(slices16, chunks)),
+                               dim3(C16_LANES, (events + C16_EPL - 1) / C16_EPL), 0, st, static_cast<const T*>(x), pk,
+                               part, index, events, g, tpb, slices16, vs16);
+          } else {
             if (events <= 2) {
               hipLaunchKernelGGL((k_wgrad_direct<T, VV, KK, CAR, SD>), dim3(blocks1d(slices, chunks)),
                                  dim3(bcg, events), 0, st, static_cast<const T*>(x), pk, part, index, events, g,
                                  tpb, slices, dk, gamma, gf32);
-              return check_launch(what);
+            } else {
+              hipLaunchKernelGGL((k_wgrad<T, VV, KK, CAR, SD>), dim3(blocks1d(slices, chunks)), dim3(bcg, events),
+                                 lds, st, static_cast<const T*>(x), pk, part, index, events, g, tpb, slices, tt, dk,
+                                 gamma, gf32);
             }
           }
-          hipLaunchKernelGGL((k_wgrad<T, VV, KK, CAR, SD>), dim3(blocks1d(slices, chunks)), dim3(bcg, events), lds,
-                             st, static_cast<const T*>(x), pk, part, index, events, g, tpb, slices, tt, dk, gamma,
-                             gf32);
           return check_launch(what);
         };
         if (!carrier && dout) return go(IC<2>{}, std::false_type{}, std::true_type{});
@@ -1284,14 +1437,15 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
   const void* ptrs[SIHC_MAX_EVENTS + 1];
   for (int i = 0; i < events; ++i) ptrs[i] = out[i];
   ptrs[events] = x;
-  const int V = pick_vec(channels, es, 8, ptrs, events + 1);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int V = pick_vec(channels, es, cell == 2 ? 8 : SIHC_RW_VEC_K4, ptrs, events + 1);
   const int S = cell * cell;
-  const Shape2D sh = shape_for(channels, V, SIHC_RW_BCG, events * S * 4);
+  const Shape2D sh = cell == 2 ? shape_for(channels, V, SIHC_RW_BCG, events * S * 4)
+                               : shape_for(channels, V, SIHC_RW_BCG_K4, events * S * 4, SIHC_RW_LDS_K4);
   const int tpb = sh.tl * SIHC_RW_TPT;
   const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
   const size_t lds = size_t(events) * S * sh.bcg * V * 4;
   const PtrPack pk = pack(ptrs, events);
-  hipStream_t st = static_cast<hipStream_t>(stream);
   return with_dtype(dtype, [&](auto t) {
     using T = decltype(t);
     return with_vec(V, [&](auto vv) {
@@ -1301,10 +1455,14 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
       } else {
         return with_cell(cell, [&](auto kk) {
           constexpr int KK = decltype(kk)::value;
-          hipLaunchKernelGGL((k_read<T, VV, KK>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), lds, st,
-                             static_cast<const T*>(x), static_cast<const T*>(alpha), pk, index, events, g, tpb,
-                             sh.slices);
-          return check_launch(what);
+          if constexpr (KK == 4 && VV > SIHC_RW_VEC_K4) {
+            return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
+          } else {
+            hipLaunchKernelGGL((k_read<T, VV, KK>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), lds, st,
+                               static_cast<const T*>(x), static_cast<const T*>(alpha), pk, index, events, g, tpb,
+                               sh.slices);
+            return check_launch(what);
+          }
         });
       }
     });
@@ -1328,16 +1486,17 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
   for (int i = 0; i < events; ++i) ptrs[i] = updates[i];
   ptrs[events] = add_x ? x : nullptr;
   ptrs[events + 1] = out;
+  hipStream_t st = static_cast<hipStream_t>(stream);
   const int es = std::max(elem_size(x_dtype), elem_size(w_dtype));
-  const int V = pick_vec(channels, es, 8, ptrs, events + 2);
+  const int V = pick_vec(channels, es, cell == 2 ? 8 : SIHC_RW_VEC_K4, ptrs, events + 2);
   const int S = cell * cell;
   const int E4 = (events + 3) & ~3;
-  const Shape2D sh = shape_for(channels, V, SIHC_RW_BCG, E4 * S * 4);
+  const Shape2D sh = cell == 2 ? shape_for(channels, V, SIHC_RW_BCG, E4 * S * 4)
+                               : shape_for(channels, V, SIHC_RW_BCG_K4, E4 * S * 4, SIHC_RW_LDS_K4);
   const int tpb = sh.tl * SIHC_RW_TPT;
   const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
   const size_t lds = size_t(E4) * S * sh.bcg * V * 4;
   const PtrPack pk = pack(updates, events);
-  hipStream_t st = static_cast<hipStream_t>(stream);
   auto launch = [&](auto tx, auto tw) {
     using TX = decltype(tx);
     using TW = decltype(tw);
@@ -1348,13 +1507,18 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
       } else {
         return with_cell(cell, [&](auto kk) {
           constexpr int KK = decltype(kk)::value;
-          return with_bool(add_x != 0, [&](auto ax) {
-            constexpr bool AX = decltype(ax)::value;
-            hipLaunchKernelGGL((k_write<TX, TW, VV, KK, AX>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl),
-                               lds, st, static_cast<const TX*>(x), pk, static_cast<const TW*>(beta),
-                               static_cast<TX*>(out), index, events, g, tpb, sh.slices);
-            return check_launch(what);
-          });
+          if constexpr (KK == 4 && VV > SIHC_RW_VEC_K4) {
+            return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
+          } else {
+            return with_bool(add_x != 0, [&](auto ax) {
+              constexpr bool AX = decltype(ax)::value;
+              hipLaunchKernelGGL((k_write<TX, TW, VV, KK, AX>), dim3(blocks1d(sh.slices, chunks)),
+                                 dim3(sh.bcg, sh.tl), lds, st, static_cast<const TX*>(x), pk,
+                                 static_cast<const TW*>(beta), static_cast<TX*>(out), index, events, g, tpb,
+                                 sh.slices);
+              return check_launch(what);
+            });
+          }
         });
       }
     });
