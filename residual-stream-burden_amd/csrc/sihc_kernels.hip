@@ -23,6 +23,10 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
+#include <map>
+#include <mutex>
+#include <tuple>
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
@@ -1206,6 +1210,57 @@ int wgrad_chunks(int64_t M, int events, int C) {
 }
 int event_bwd_chunks(int64_t M) { return chunk_count(M, SIHC_EV_CHUNK, 512); }
 
+// Compute units of the current device (cached per device; 0 if unknown).
+int device_cus() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0 && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess)
+    cus[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// Blocks of `kernel` (at this block size and dynamic LDS) resident on the whole device
+// at once; 0 if the runtime cannot tell. Cached per (kernel, block size, LDS).
+int resident_blocks(const void* kernel, int threads, size_t lds) {
+  struct Key {
+    const void* k;
+    int threads;
+    size_t lds;
+    bool operator<(const Key& o) const {
+      return std::tie(k, threads, lds) < std::tie(o.k, o.threads, o.lds);
+    }
+  };
+  static std::mutex mu;
+  static std::map<Key, int> cache;
+  const Key key{kernel, threads, lds};
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second * device_cus();
+  }
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  cache[key] = per_cu;
+  return per_cu * device_cus();
+}
+
+// Chunk count <= max_chunks for which slices x chunks blocks form a whole number of
+// rounds of `resident` blocks, so no round runs part-empty (a grid of 4.5 rounds
+// leaves half the device idle for its last tenth). max_chunks when unknown or when the
+// grid is under one round.
+int whole_rounds(int slices, int max_chunks, int resident) {
+  if (resident <= 0) return max_chunks;
+  const int64_t rounds = int64_t(slices) * max_chunks / resident;
+  if (rounds < 1) return max_chunks;
+  return int(std::max<int64_t>(1, rounds * resident / slices));
+}
+
 int check_geometry(const char* what, int64_t batch, int grid, int cell, int channels, Geo* g) {
   if (batch < 0 || grid <= 0 || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
   if (cell != 2 && cell != 4) return fail(SIHC_ERR_INVALID, "%s: cell must be 2 or 4 (4 or 16 slots)", what);
@@ -1729,10 +1784,11 @@ int sihc_event_backward(const void* grad_x_out, const void* grad_z_out, const vo
   if (!has_w && !has_g) return fail(SIHC_ERR_INVALID, "%s: neither a write nor a read part", what);
   if (!grad_x && has_g)
     return fail(SIHC_ERR_INVALID, "%s: grad_x may be NULL only without grad_z_out (it equals grad_x_out)", what);
-  const int chunks = event_bwd_chunks(g.M);
-  const size_t need = size_t(chunks) * 2 * S * channels * sizeof(float);
+  const int max_chunks = event_bwd_chunks(g.M);
+  const size_t need = size_t(max_chunks) * 2 * S * channels * sizeof(float);
   if (!workspace || workspace_bytes < need)
     return fail(SIHC_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", what, need, workspace_bytes);
+  int chunks = max_chunks;
   if (!aligned(workspace, 16)) return fail(SIHC_ERR_INVALID, "%s: workspace must be 16-byte aligned", what);
   const int es = elem_size(dtype);
   if ((beta && !aligned(beta, std::min(16, S * es))) || (alpha_next && !aligned(alpha_next, std::min(16, S * es))))
@@ -1743,7 +1799,6 @@ int sihc_event_backward(const void* grad_x_out, const void* grad_z_out, const vo
                    (has_g && !aligned(alpha_next, std::min(16, V * S * es)))))
     V /= 2;
   const Shape2D sh = shape_for(channels, V, SIHC_EV_BCG, 0);
-  const int tpb = int((int64_t(g.M) + chunks - 1) / chunks);
   const size_t lds = size_t(sh.tl) * sh.bcg * S * V * sizeof(float);  // TL x (BCG*S*V) floats
   float* part = static_cast<float*>(workspace);
   const bool store_t = grad_x != nullptr;
@@ -1762,6 +1817,9 @@ int sihc_event_backward(const void* grad_x_out, const void* grad_z_out, const vo
             constexpr bool HH = decltype(hh)::value;
             auto go = [&](auto hg, auto hw, auto stt) {
               constexpr bool HG = decltype(hg)::value, HW = decltype(hw)::value, STT = decltype(stt)::value;
+              const void* kfn = reinterpret_cast<const void*>(&k_event_bwd<T, VV, KK, HH, HG, HW, STT>);
+              chunks = whole_rounds(sh.slices, max_chunks, resident_blocks(kfn, sh.bcg * sh.tl, lds));
+              const int tpb = int((int64_t(g.M) + chunks - 1) / chunks);
               hipLaunchKernelGGL((k_event_bwd<T, VV, KK, HH, HG, HW, STT>), dim3(blocks1d(sh.slices, chunks)),
                                  dim3(sh.bcg, sh.tl), lds, st, static_cast<const T*>(grad_x_out),
                                  static_cast<const T*>(grad_z_out), static_cast<const T*>(x_out),
