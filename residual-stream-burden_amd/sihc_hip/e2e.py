@@ -1,14 +1,18 @@
 """Compact SiHC sublayer denoiser whose routing runs on the HIP ops.
 
 Architecture (behaviour of tongtongliang/residual-stream-burden
-sihc/models/sihc/sublayer.py:30-72, model.py:186-531 and components.py:14-324):
+sihc/models/sihc/sublayer.py:30-128, model.py:186-682 and components.py:14-324):
 a patch stem maps a 256x256x3 image to the NHWC carrier [B, 256/p, 256/p, D]; each of
 `depth` blocks has an AdaLN-modulated attention update and a SwiGLU MLP update
 computed on the 16x16 workspace, each with its own static connection (read/write
 weights [D, S]); stages of 8 or 12 blocks are routed either with the reference's
 late-materialised schedule (read -> triangular -> write, `schedule="stage"`) or with
 the per-event fused schedule (`schedule="literal"`); a modulated final layer maps the
-carrier back to image space.
+carrier back to image space. With `in_context_len > 0` (the in-context variant,
+model.py:565-682, sublayer.py:75-128) class-embedding prefix tokens join the workspace
+sequence from block `in_context_start` on: attention and MLP run on
+[prefix, workspace], the prefix takes ordinary residual updates and never enters the
+routing, and its RoPE positions are unrotated (components.py:44-70).
 
 The bodies are plain PyTorch (they are not part of the read/write path). Routing
 calls go through three replaceable hooks (`read`, `triangular`, `write`), so tests
@@ -129,12 +133,17 @@ class Block(nn.Module):
 class SiHCDenoiser(nn.Module):
     def __init__(self, hidden: int = 1152, depth: int = 28, heads: int = 16, patch: int = 8,
                  stages: tuple[int, ...] = (8, 12, 8), mlp_ratio: float = 4.0, num_classes: int = 1000,
-                 image: int = 256, grid: int = 16, schedule: str = "stage"):
+                 image: int = 256, grid: int = 16, schedule: str = "stage", in_context_len: int = 0,
+                 in_context_start: int = 4):
         super().__init__()
         if sum(stages) != depth or any(s not in (8, 12) for s in stages):
             raise ValueError("stages must be 8 or 12 blocks each and sum to depth")
         if schedule not in ("stage", "literal"):
             raise ValueError("schedule must be 'stage' or 'literal'")
+        if in_context_len < 0:
+            raise ValueError(f"in_context_len must be >= 0, got {in_context_len}")
+        if in_context_len and not 0 <= in_context_start < depth:
+            raise ValueError(f"in_context_start must be in [0, {depth}), got {in_context_start}")
         self.hidden, self.patch, self.image, self.grid = hidden, patch, image, grid
         self.cell = image // patch // grid
         self.slots = self.cell * self.cell
@@ -150,6 +159,13 @@ class SiHCDenoiser(nn.Module):
         cos, sin = rope_tables(hidden // heads, grid)
         self.register_buffer("rope_cos", cos, persistent=False)
         self.register_buffer("rope_sin", sin, persistent=False)
+        self.in_context_len, self.in_context_start = int(in_context_len), int(in_context_start)
+        if self.in_context_len:
+            self.in_context_posemb = nn.Parameter(torch.zeros(1, self.in_context_len, hidden))
+            # prefix positions are not rotated
+            pre = self.in_context_len
+            self.register_buffer("rope_cos_ctx", torch.cat([torch.ones(pre, cos.shape[1]), cos]), persistent=False)
+            self.register_buffer("rope_sin_ctx", torch.cat([torch.zeros(pre, sin.shape[1]), sin]), persistent=False)
         # routing hooks (None: the HIP ops) and optional timing of routing calls
         self.read = self.triangular = self.write = None
         self.routing_timer: Optional[list] = None
@@ -177,7 +193,24 @@ class SiHCDenoiser(nn.Module):
         self.routing_timer.append((start, end))
         return out
 
-    def _stage_schedule(self, x0, cond, blocks, cos, sin):
+    def _update(self, block, part, z, mod, context, index):
+        """One sublayer's workspace update (and the prefix tokens' new state): the body
+        runs on [prefix, workspace] from block `in_context_start` on (sublayer.py:97-114)."""
+        use_context = context is not None and index >= self.in_context_start
+        if use_context:
+            seq = torch.cat((context, z), dim=1)
+            cos, sin = self.rope_cos_ctx.to(z.dtype), self.rope_sin_ctx.to(z.dtype)
+        else:
+            seq = z
+            cos, sin = self.rope_cos.to(z.dtype), self.rope_sin.to(z.dtype)
+        dseq = block.attention_update(seq, mod, cos, sin) if part == 0 else block.mlp_update(seq, mod)
+        if not use_context:
+            return dseq.contiguous(), context
+        pre = self.in_context_len
+        # removing the prefix leaves a batch-strided view: the routing ops need it packed
+        return dseq[:, pre:].contiguous(), context + dseq[:, :pre]
+
+    def _stage_schedule(self, x0, cond, blocks, first, context):
         conns = [c for b in blocks for c in (b.attention_connection, b.mlp_connection)]
         alpha = torch.stack([c.read_weight.to(x0.dtype) for c in conns]).contiguous()
         beta = torch.stack([c.write_weight.to(x0.dtype) for c in conns]).contiguous()
@@ -194,27 +227,27 @@ class SiHCDenoiser(nn.Module):
                 z = base[e]
                 if updates:
                     z = self._timed(tri, z, updates, gamma[e, :e].contiguous())
-                dz = block.attention_update(z, mod, cos, sin) if part == 0 else block.mlp_update(z, mod)
-                updates.append(dz.contiguous())
-        return self._timed(write, x0, updates, beta)
+                dz, context = self._update(block, part, z, mod, context, first + i)
+                updates.append(dz)
+        return self._timed(write, x0, updates, beta), context
 
-    def _literal_schedule(self, x0, cond, blocks, cos, sin):
+    def _literal_schedule(self, x0, cond, blocks, first, context):
         conns = [c for b in blocks for c in (b.attention_connection, b.mlp_connection)]
         alpha = [c.read_weight.to(x0.dtype).contiguous() for c in conns]
         beta = [c.write_weight.to(x0.dtype).contiguous() for c in conns]
         z = self._timed(self.read or sublayer_read, x0, alpha[0][None])[0]
         x = x0
         e = 0
-        for block in blocks:
+        for i, block in enumerate(blocks):
             mod = block.ada(cond).chunk(6, dim=-1)
             for part in range(2):
-                dz = (block.attention_update(z, mod, cos, sin) if part == 0 else block.mlp_update(z, mod)).contiguous()
+                dz, context = self._update(block, part, z, mod, context, first + i)
                 if e + 1 < len(conns):
                     x, z = self._timed(event_write_read, x, dz, beta[e], alpha[e + 1])
                 else:
                     x = self._timed(self.write or sublayer_write, x, [dz], beta[e][None])
                 e += 1
-        return x
+        return x, context
 
     def forward(self, x, t, y):
         b = x.shape[0]
@@ -223,15 +256,17 @@ class SiHCDenoiser(nn.Module):
         freqs = torch.exp(-math.log(10000.0) * torch.arange(half, device=t.device, dtype=torch.float32) / half)
         args = t.float()[:, None] * freqs[None]
         temb = torch.cat([args.cos(), args.sin()], dim=-1).to(self.stem.weight.dtype)
-        cond = self.t_mlp(temb) + self.y_table(y)
+        y_emb = self.y_table(y)
+        cond = self.t_mlp(temb) + y_emb
         patches = x.reshape(b, 3, hi, p, hi, p).permute(0, 2, 4, 1, 3, 5).reshape(b, hi, hi, 3 * p * p)
         carrier = self.stem(patches.to(self.stem.weight.dtype)).contiguous()
-        cos = self.rope_cos.to(carrier.dtype)
-        sin = self.rope_sin.to(carrier.dtype)
+        context = None
+        if self.in_context_len:  # model.py:674-676
+            context = (y_emb[:, None].expand(-1, self.in_context_len, -1) + self.in_context_posemb).to(carrier.dtype)
         run = self._stage_schedule if self.schedule == "stage" else self._literal_schedule
         start = 0
         for size in self.stages:
-            carrier = run(carrier, cond, list(self.blocks[start:start + size]), cos, sin)
+            carrier, context = run(carrier, cond, list(self.blocks[start:start + size]), start, context)
             start += size
         shift, scale = self.final_ada(cond).chunk(2, dim=-1)
         out = self.final(_modulate(self.final_norm(carrier.reshape(b, hi * hi, self.hidden)), shift, scale))

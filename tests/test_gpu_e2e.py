@@ -89,3 +89,98 @@ def test_xl_shape_forward_runs(schedule):
     with torch.no_grad():
         out = model(x.bfloat16(), t, y)
     assert out.shape == (2, 3, 256, 256) and torch.isfinite(out.float()).all()
+
+
+def _ctx(schedule, seed=0, depth=8):
+    torch.manual_seed(seed)
+    stages = (8,) if depth == 8 else (8, 12)
+    return SiHCDenoiser(hidden=64, depth=depth, heads=4, patch=8, stages=stages, schedule=schedule,
+                        in_context_len=4, in_context_start=2).random_init(seed=seed).cuda()
+
+
+@pytest.mark.parametrize("schedule", ["stage", "literal"])
+def test_in_context_model_matches_oracle_routing_fp32(schedule):
+    # SublayerSiHCInContextModel behaviour (sublayer.py:84-128): prefix tokens join the
+    # workspace sequence from block 2 on and never enter the routing.
+    announce(f"e2e in-context {schedule} fp32")
+    model = _ctx(schedule, depth=20)
+    ref = _oracle_routing(copy.deepcopy(model))
+    ref.schedule = "stage"  # the oracle routes the same recurrence late-materialised
+    x, t, y = _inputs()
+    out, expected = model(x, t, y), ref(x, t, y)
+    out.float().square().mean().backward()
+    expected.float().square().mean().backward()
+    assert rel_l2(out, expected) < 1e-5
+    for (name, a), (_, b) in zip(model.named_parameters(), ref.named_parameters()):
+        assert a.grad is not None and torch.isfinite(a.grad).all(), name
+        assert rel_l2(a.grad, b.grad) < 1e-4, (name, rel_l2(a.grad, b.grad))
+    assert model.in_context_posemb.grad.abs().sum() > 0
+
+
+@pytest.mark.parametrize("schedule", ["stage", "literal"])
+def test_whole_model_fullgraph_compile(schedule):
+    # The whole denoiser (bodies + HIP routing ops) traced without a graph break; the
+    # routing ops run through their fake implementations at trace time.
+    announce(f"e2e fullgraph compile {schedule}")
+    torch._dynamo.reset()
+    model = _ctx(schedule)
+    twin = copy.deepcopy(model)
+    x, t, y = _inputs()
+    eager = model(x, t, y)
+    eager.float().square().mean().backward()
+    compiled = torch.compile(twin, backend="aot_eager", fullgraph=True)
+    out = compiled(x, t, y)
+    out.float().square().mean().backward()
+    assert rel_l2(out, eager) < 1e-6
+    for (name, a), (_, b) in zip(twin.named_parameters(), model.named_parameters()):
+        assert rel_l2(a.grad, b.grad) < 1e-5, (name, rel_l2(a.grad, b.grad))
+
+
+def test_model_forward_hip_graph_replay():
+    # Inference forward captured once and replayed on new inputs (the reference's
+    # CUDA-graph sampling path, sampling.py:6-11), with eager work between replays.
+    announce("e2e hip graph forward")
+    model = _ctx("literal").to(torch.bfloat16).eval()
+    x, t, y = _inputs()
+    sx, st, sy = x.bfloat16().clone(), t.clone(), y.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.no_grad(), torch.cuda.stream(side):
+        for _ in range(2):
+            model(sx, st, sy)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.graph(graph):
+        static_out = model(sx, st, sy)
+    for r in range(3):
+        nx, nt, ny = _inputs(seed=10 + r)
+        sx.copy_(nx.bfloat16())
+        st.copy_(nt)
+        sy.copy_(ny)
+        graph.replay()
+        with torch.no_grad():
+            expected = model(nx.bfloat16(), nt, ny)
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, expected), f"replay {r} differs from eager"
+
+
+def test_checkpoint_round_trip(tmp_path):
+    # state_dict -> file -> weights-only load into a fresh model: identical outputs.
+    # The connection parameters keep the reference's names and layout
+    # (blocks.{i}.{attention,mlp}_connection.{read,write}_weight, [D, S] fp32).
+    announce("e2e checkpoint round trip")
+    model = _ctx("stage", seed=3)
+    path = tmp_path / "ckpt.pt"
+    torch.save(model.state_dict(), path)
+    fresh = SiHCDenoiser(hidden=64, depth=8, heads=4, patch=8, stages=(8,), in_context_len=4,
+                         in_context_start=2).cuda()
+    fresh.load_state_dict(torch.load(path, weights_only=True))
+    x, t, y = _inputs()
+    with torch.no_grad():
+        assert torch.equal(model(x, t, y), fresh(x, t, y))
+    keys = set(fresh.state_dict())
+    for i in range(8):
+        for conn in ("attention_connection", "mlp_connection"):
+            for w in ("read_weight", "write_weight"):
+                k = f"blocks.{i}.{conn}.{w}"
+                assert k in keys and fresh.state_dict()[k].shape == (64, 4) and fresh.state_dict()[k].dtype == torch.float32
