@@ -55,11 +55,18 @@ def parse_args():
                    help="routing schedule of --mode e2e")
     p.add_argument("--slots", type=int, choices=(4, 16), default=4,
                    help="cell slots of --mode kernels: 4 (p8, 32x32 carrier) or 16 (p4, 64x64 carrier)")
-    p.add_argument("--mode", choices=("step", "calibrate", "kernels", "e2e"), default="step",
+    p.add_argument("--size", default="B,XL", help="--mode model: presets among B,L,XL,H")
+    p.add_argument("--implementation", default="literal,factored,fused,event",
+                   help="--mode model: routing implementations")
+    p.add_argument("--phase", default="train,inference", help="--mode model: train and/or inference")
+    p.add_argument("--model-batch", type=int, default=128, help="--mode model: images per step")
+    p.add_argument("--no-graph", action="store_true", help="--mode model: inference without HIP-graph capture")
+    p.add_argument("--mode", choices=("step", "calibrate", "kernels", "e2e", "model"), default="step",
                    help="step: the benchmark (default); calibrate: a 1 GiB copy-kernel launch plus single "
                         "event forward/backward launches at the same shape, for HBM counter runs; kernels: "
                         "every HIP kernel timed alone at the benchmark shape (one JSON line per kernel); e2e: "
-                        "BASELINE config 4, a SiHC-XL denoiser forward on a CFG batch with HIP routing")
+                        "BASELINE config 4, a SiHC-XL denoiser forward on a CFG batch with HIP routing; model: the "
+                        "reference's fusion_profile matrix (presets x routing implementation x train/inference)")
     return p.parse_args()
 
 
@@ -496,6 +503,151 @@ def e2e_config4(seed: int, schedules=("stage", "literal"), steps: int = 5) -> di
     return out
 
 
+# ---- model-level benchmark (the reference's sihc/bench/fusion_profile.py matrix)
+# Presets of sihc/presets.py:9-23: (depth, hidden, heads, stage sizes, in-context start);
+# every preset is patch 4 (16-slot cells) with 32 in-context prefix tokens.
+MODEL_PRESETS = {
+    "B": (12, 768, 12, (12,), 4),
+    "L": (24, 1024, 16, (12, 12), 8),
+    "XL": (40, 1024, 16, (8, 8, 8, 8, 8), 8),
+    "H": (32, 1280, 16, (8, 12, 12), 8),
+}
+
+
+def _torch_controls():
+    """The reference's PyTorch routing controls (sihc/bench/fusion_controls.py:14-38),
+    run on the GPU as the unfused baselines of the model benchmark: NHWC reshapes,
+    fp32 products, one cast. Benchmark controls only; the library never calls them."""
+
+    def read(x, alpha_cs):
+        b, h, _, c = x.shape
+        k = int(round(alpha_cs.shape[1] ** 0.5))
+        g = h // k
+        cells = x.reshape(b, g, k, g, k, c)
+        w = alpha_cs.T.reshape(1, 1, k, 1, k, c)
+        return (cells.float() * w.float()).sum((2, 4)).reshape(b, g * g, c).to(x.dtype)
+
+    def write(x, updates, betas):
+        b, h, _, c = x.shape
+        k = int(round(betas[0].shape[1] ** 0.5))
+        g = h // k
+        value = x.reshape(b, g, k, g, k, c).float()
+        for dz, beta in zip(updates, betas):
+            value = value + dz.reshape(b, g, 1, g, 1, c).float() * beta.T.reshape(1, 1, k, 1, k, c).float()
+        return value.reshape_as(x).to(x.dtype)
+
+    def triangular(base, updates, gamma):
+        value = base.float()
+        for j, dz in enumerate(updates):
+            value = value + dz.float() * gamma[j].float()
+        return value.to(base.dtype)
+
+    return read, write, triangular
+
+
+def model_step(size: str, implementation: str, phase: str, batch: int, steps: int, warmup: int,
+               graph: bool, seed: int) -> dict:
+    """One fusion_profile cell on this GPU: the compact SiHC sublayer denoiser of
+    sihc_hip.e2e at a reference preset, FP32 parameters under BF16 autocast, batch
+    `batch`. train: forward, loss, backward, fused AdamW (lr 2e-4, betas 0.9/0.95) and
+    two FP32 EMAs; inference: one forward (HIP-graph captured with `graph`). Routing:
+    fused = HIP stage API (reference "fused"), event = HIP per-event schedule,
+    factored / literal = the PyTorch controls (reference "factored" / "literal").
+    Bodies run eager (no tracing compiler)."""
+    import torch
+
+    from sihc_hip.e2e import SiHCDenoiser
+
+    depth, hidden, heads, stages, ctx_start = MODEL_PRESETS[size]
+    schedule = "stage" if implementation in ("fused", "factored") else "literal"
+    dev = torch.device("cuda", 0)
+    torch.manual_seed(seed)
+    torch.cuda.reset_peak_memory_stats()
+    model = SiHCDenoiser(hidden=hidden, depth=depth, heads=heads, patch=4, stages=stages, schedule=schedule,
+                         in_context_len=32, in_context_start=ctx_start).random_init(seed=seed).to(dev)
+    if implementation in ("factored", "literal"):
+        read, write, tri = _torch_controls()
+        model.read = lambda x, alpha: [read(x, a) for a in alpha.unbind(0)]
+        model.triangular = tri
+        model.write = lambda x, ups, beta: write(x, ups, list(beta.unbind(0)))
+        model.event = lambda x, dz, b, a: (lambda xo: (xo, read(xo, a)))(write(x, [dz], [b]))
+    g = torch.Generator(device=dev).manual_seed(seed + 1)
+    x = torch.randn(batch, 3, 256, 256, device=dev, generator=g)
+    t = torch.full((batch,), 0.5, device=dev)
+    y = torch.arange(batch, device=dev) % 1000
+    out = {"size": size, "implementation": implementation, "phase": phase, "batch": batch,
+           "params": sum(p.numel() for p in model.parameters())}
+    if phase == "train":
+        model.train()
+        target = torch.randn(batch, 3, 256, 256, device=dev, generator=g)
+        params = [p for p in model.parameters() if p.requires_grad]
+        opt = torch.optim.AdamW(params, lr=2e-4, betas=(0.9, 0.95), weight_decay=0, fused=True)
+        emas = [[p.detach().clone() for p in params] for _ in range(2)]
+
+        def run():
+            opt.zero_grad(set_to_none=True)
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                loss = (model(x, t, y).float() - target).square().flatten(1).mean(1).mean()
+            loss.backward()
+            opt.step()
+            with torch.no_grad():
+                for copies, decay in zip(emas, (0.9999, 0.9996)):
+                    torch._foreach_mul_(copies, decay)
+                    torch._foreach_add_(copies, params, alpha=1 - decay)
+            return loss
+    else:
+        model.eval().requires_grad_(False)
+        if graph:
+            static = [x.clone(), t.clone(), y.clone()]
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            # autocast's weight-cast cache off: the casts are recorded into the graph
+            amp = dict(device_type="cuda", dtype=torch.bfloat16, cache_enabled=False)
+            with torch.inference_mode(), torch.cuda.stream(side), torch.autocast(**amp):
+                for _ in range(2):
+                    model(*static)
+            torch.cuda.current_stream().wait_stream(side)
+            hg = torch.cuda.CUDAGraph()
+            with torch.inference_mode(), torch.cuda.graph(hg), torch.autocast(**amp):
+                result = model(*static)
+
+            def run():
+                hg.replay()
+                return result
+        else:
+            def run():
+                with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
+                    return model(x, t, y)
+    last = None
+    for _ in range(warmup):
+        last = run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        last = run()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    finite = bool(torch.isfinite(last.float()).all())
+    out.update({"ms_per_step": round(dt * 1e3, 2), "images_per_s": round(batch / dt, 1),
+                "peak_allocated_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2), "finite": finite,
+                "hip_graph": bool(graph and phase == "inference")})
+    return out
+
+
+def model_bench(args) -> None:
+    for size in args.size.split(","):
+        for phase in args.phase.split(","):
+            for impl in args.implementation.split(","):
+                import torch
+                try:
+                    r = model_step(size, impl, phase, args.model_batch, args.steps, args.warmup,
+                                   not args.no_graph, args.seed)
+                except torch.OutOfMemoryError:
+                    r = {"size": size, "implementation": impl, "phase": phase, "status": "oom"}
+                print(json.dumps(r), flush=True)
+                torch.cuda.empty_cache()
+
+
 def e2e(args) -> None:
     print(json.dumps(e2e_config4(args.seed, (args.schedule,), max(1, min(args.steps, 10)))), flush=True)
 
@@ -520,6 +672,9 @@ def main():
         return
     if args.mode == "e2e":
         e2e(args)
+        return
+    if args.mode == "model":
+        model_bench(args)
         return
     print(f"[bench] building step: batch={args.batch} C={args.channels} events={args.events}", file=sys.stderr,
           flush=True)

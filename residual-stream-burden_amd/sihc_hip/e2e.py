@@ -15,9 +15,10 @@ sequence from block `in_context_start` on: attention and MLP run on
 routing, and its RoPE positions are unrotated (components.py:44-70).
 
 The bodies are plain PyTorch (they are not part of the read/write path). Routing
-calls go through three replaceable hooks (`read`, `triangular`, `write`), so tests
-can swap in other implementations of the same functions, and an optional list of HIP
-event pairs records the time spent in routing.
+calls go through replaceable hooks (`read`, `triangular`, `write`, and `event` for the
+per-event write+read), so tests and benchmarks can swap in other implementations of
+the same functions, and an optional list of HIP event pairs records the time spent in
+routing.
 """
 from __future__ import annotations
 
@@ -167,7 +168,7 @@ class SiHCDenoiser(nn.Module):
             self.register_buffer("rope_cos_ctx", torch.cat([torch.ones(pre, cos.shape[1]), cos]), persistent=False)
             self.register_buffer("rope_sin_ctx", torch.cat([torch.zeros(pre, sin.shape[1]), sin]), persistent=False)
         # routing hooks (None: the HIP ops) and optional timing of routing calls
-        self.read = self.triangular = self.write = None
+        self.read = self.triangular = self.write = self.event = None
         self.routing_timer: Optional[list] = None
 
     def random_init(self, std: float = 0.02, seed: int = 0) -> "SiHCDenoiser":
@@ -243,7 +244,7 @@ class SiHCDenoiser(nn.Module):
             for part in range(2):
                 dz, context = self._update(block, part, z, mod, context, first + i)
                 if e + 1 < len(conns):
-                    x, z = self._timed(event_write_read, x, dz, beta[e], alpha[e + 1])
+                    x, z = self._timed(self.event or event_write_read, x, dz, beta[e], alpha[e + 1])
                 else:
                     x = self._timed(self.write or sublayer_write, x, [dz], beta[e][None])
                 e += 1
