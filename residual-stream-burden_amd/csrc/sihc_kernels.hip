@@ -82,6 +82,10 @@
 #ifndef SIHC_WG_CHUNK  // tokens per reduction chunk, weight / gamma gradients
 #define SIHC_WG_CHUNK 512
 #endif
+#ifndef SIHC_WG_TT  // most tokens per staged LDS tile of the weight / gamma gradients
+#define SIHC_WG_TT 32
+#endif
+
 #ifndef SIHC_NT  // 1: non-temporal (streaming) hints on carrier/workspace traffic
 #define SIHC_NT 0
 #endif
@@ -280,7 +284,7 @@ __device__ __forceinline__ void stage_weights(float* lds, const TW* __restrict__
 // read: out_e[m,c] = sum_s alpha[e,c,s] * x[m,s,c]
 // 1-D grid of (slices x chunks), block (BCG, TL); LDS holds alpha as [E][S][BC] fp32.
 // ----------------------------------------------------------------------------------
-template <typename T, int V, int K>
+template <typename T, int V, int K, int BCGT>
 __global__ void __launch_bounds__(256) k_read(const T* __restrict__ x, const T* __restrict__ alpha,
                                               PtrPack out, const int32_t* __restrict__ index,
                                               int E, Geo g, int tpb, int nslices) {
@@ -288,7 +292,9 @@ __global__ void __launch_bounds__(256) k_read(const T* __restrict__ x, const T* 
   // tokens per lane per iteration: each LDS weight feeds U tokens
   constexpr int U = K == 2 ? SIHC_RW_UNROLL : SIHC_RW_UNROLL_K4;
   extern __shared__ float lds[];
-  const int BCG = blockDim.x, TL = blockDim.y;
+  // BCGT: channel-group lanes known at compile time (0: blockDim.x), so LDS row strides
+  // fold into the ds_read immediate offsets instead of costing an add per weight row
+  const int BCG = BCGT ? BCGT : int(blockDim.x), TL = blockDim.y;
   const int BC = BCG * V;
   const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
   const int cs = slice * BC;
@@ -338,7 +344,7 @@ __global__ void __launch_bounds__(256) k_read(const T* __restrict__ x, const T* 
 // Events are consumed in groups of 4 (E padded to a multiple of 4 with zero weights
 // and a repeated valid pointer), so each group's 4 update loads issue together.
 // ----------------------------------------------------------------------------------
-template <typename TX, typename TW, int V, int K, bool ADD_X>
+template <typename TX, typename TW, int V, int K, bool ADD_X, int BCGT>
 __global__ void __launch_bounds__(256) k_write(const TX* __restrict__ x, PtrPack upd,
                                                const TW* __restrict__ beta, TX* __restrict__ out,
                                                const int32_t* __restrict__ index, int E, Geo g, int tpb,
@@ -348,7 +354,7 @@ __global__ void __launch_bounds__(256) k_write(const TX* __restrict__ x, PtrPack
   constexpr int U = K == 2 ? SIHC_RW_UNROLL : SIHC_RW_UNROLL_K4;
   constexpr int EG = U > 1 ? 2 : 4;  // events per load group
   extern __shared__ float lds[];
-  const int BCG = blockDim.x, TL = blockDim.y;
+  const int BCG = BCGT ? BCGT : int(blockDim.x), TL = blockDim.y;  // BCGT as in k_read
   const int BC = BCG * V;
   const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
   const int cs = slice * BC;
@@ -1317,6 +1323,18 @@ int with_cell(int k, F&& f) {
   if (k == 2) return f(IC<2>{});
   return f(IC<4>{});
 }
+// Compile-time lane counts of the 16-slot read / write (0: runtime value). Measured: a
+// known lane count saves the per-row LDS address adds at 16 slots (write E=24 3.6 -> 3.2
+// ms); at 4 slots it raises register use and occupancy drops, so those stay runtime.
+template <int K, typename F>
+int with_bcg(int bcg, F&& f) {
+  if constexpr (K == 4) {
+    if (bcg == 32) return f(IC<32>{});
+    if (bcg == 16) return f(IC<16>{});
+  }
+  return f(IC<0>{});
+}
+
 template <typename F>
 int with_bool(bool b, F&& f) {
   if (b) return f(std::true_type{});
@@ -1414,7 +1432,7 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
   const int tpb = int((int64_t(g.M) + chunks - 1) / chunks);
   // x tile of TT tokens: at most 32 KB of LDS.
   int tt = 32768 / (S * bcg * V * int(sizeof(float)));
-  tt = std::max(1, std::min(tt, 32));
+  tt = std::max(1, std::min(tt, SIHC_WG_TT));
   const size_t lds = size_t(tt) * S * bcg * V * sizeof(float);
   const PtrPack pk = pack(z, events);
   const PtrPack dk = dout ? pack(const_cast<const void* const*>(dout), events) : PtrPack{};
@@ -1513,10 +1531,13 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
           if constexpr (KK == 4 && VV > SIHC_RW_VEC_K4) {
             return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
           } else {
-            hipLaunchKernelGGL((k_read<T, VV, KK>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), lds, st,
-                               static_cast<const T*>(x), static_cast<const T*>(alpha), pk, index, events, g, tpb,
-                               sh.slices);
-            return check_launch(what);
+            return with_bcg<KK>(sh.bcg, [&](auto bb) {
+              constexpr int BB = decltype(bb)::value;
+              hipLaunchKernelGGL((k_read<T, VV, KK, BB>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), lds,
+                                 st, static_cast<const T*>(x), static_cast<const T*>(alpha), pk, index, events, g,
+                                 tpb, sh.slices);
+              return check_launch(what);
+            });
           }
         });
       }
@@ -1567,11 +1588,14 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
           } else {
             return with_bool(add_x != 0, [&](auto ax) {
               constexpr bool AX = decltype(ax)::value;
-              hipLaunchKernelGGL((k_write<TX, TW, VV, KK, AX>), dim3(blocks1d(sh.slices, chunks)),
-                                 dim3(sh.bcg, sh.tl), lds, st, static_cast<const TX*>(x), pk,
-                                 static_cast<const TW*>(beta), static_cast<TX*>(out), index, events, g, tpb,
-                                 sh.slices);
-              return check_launch(what);
+              return with_bcg<KK>(sh.bcg, [&](auto bb) {
+                constexpr int BB = decltype(bb)::value;
+                hipLaunchKernelGGL((k_write<TX, TW, VV, KK, AX, BB>), dim3(blocks1d(sh.slices, chunks)),
+                                   dim3(sh.bcg, sh.tl), lds, st, static_cast<const TX*>(x), pk,
+                                   static_cast<const TW*>(beta), static_cast<TX*>(out), index, events, g, tpb,
+                                   sh.slices);
+                return check_launch(what);
+              });
             });
           }
         });
