@@ -20,7 +20,8 @@
  *
  * dtype codes: SIHC_DTYPE_F32 (IEEE fp32) and SIHC_DTYPE_BF16 (bfloat16). All
  * arithmetic accumulates in fp32 and rounds once (round-to-nearest-even) per stored
- * element. Pointer arrays (`updates`, `out`) are host arrays of `events` device
+ * element; a NaN stored as bf16 is a quiet NaN with the sign and top payload bits of
+ * the NaN that produced it. Pointer arrays (`updates`, `out`) are host arrays of `events` device
  * pointers; at most SIHC_MAX_EVENTS.
  *
  * Reference: tongtongliang/residual-stream-burden, sihc/models/sihc/sublayer_kernels.py

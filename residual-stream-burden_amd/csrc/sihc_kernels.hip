@@ -92,6 +92,12 @@
 #ifndef SIHC_LOAD_FENCE  // 1: keep each token's loads ahead of its arithmetic (see load_fence)
 #define SIHC_LOAD_FENCE 1
 #endif
+#ifndef SIHC_HW_BF16  // 1: fp32 -> bf16 stores through the hardware conversion instruction
+#define SIHC_HW_BF16 1
+#endif
+#ifndef SIHC_RW_MINW  // minimum waves per SIMD read / write are compiled for (caps VGPRs)
+#define SIHC_RW_MINW 3
+#endif
 
 namespace {
 
@@ -112,12 +118,19 @@ template <>
 __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <>
 __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {
+#if SIHC_HW_BF16
+  // gfx950's v_cvt_pk_bf16_f32 (the compiler pairs adjacent conversions): round to
+  // nearest, ties to even, identical to the software path below for every non-NaN
+  // input; a NaN keeps its sign and top payload bits (quieted).
+  return __builtin_bit_cast(bf16_t, static_cast<__bf16>(v));
+#else
   // Round to nearest, ties to even; every NaN becomes the canonical quiet NaN 0x7fc0
   // (the same bits torch's float->bfloat16 conversion produces).
   uint32_t u = __float_as_uint(v);
   if ((u & 0x7fffffffu) > 0x7f800000u) return bf16_t(0x7fc0);
   u += 0x7fffu + ((u >> 16) & 1u);
   return bf16_t(u >> 16);
+#endif
 }
 // Scheduling fence between a token's load phase and its arithmetic. Without it the
 // compiler interleaves loads with the math that consumes them to save registers,
@@ -285,7 +298,7 @@ __device__ __forceinline__ void stage_weights(float* lds, const TW* __restrict__
 // 1-D grid of (slices x chunks), block (BCG, TL); LDS holds alpha as [E][S][BC] fp32.
 // ----------------------------------------------------------------------------------
 template <typename T, int V, int K, int BCGT>
-__global__ void __launch_bounds__(256) k_read(const T* __restrict__ x, const T* __restrict__ alpha,
+__global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict__ x, const T* __restrict__ alpha,
                                               PtrPack out, const int32_t* __restrict__ index,
                                               int E, Geo g, int tpb, int nslices) {
   constexpr int S = K * K;
@@ -345,7 +358,7 @@ __global__ void __launch_bounds__(256) k_read(const T* __restrict__ x, const T* 
 // and a repeated valid pointer), so each group's 4 update loads issue together.
 // ----------------------------------------------------------------------------------
 template <typename TX, typename TW, int V, int K, bool ADD_X, int BCGT>
-__global__ void __launch_bounds__(256) k_write(const TX* __restrict__ x, PtrPack upd,
+__global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restrict__ x, PtrPack upd,
                                                const TW* __restrict__ beta, TX* __restrict__ out,
                                                const int32_t* __restrict__ index, int E, Geo g, int tpb,
                                                int nslices) {
