@@ -731,8 +731,8 @@ __global__ void __launch_bounds__(512) k_wgrad16(const T* __restrict__ x, PtrPac
                                                  int nslices, int vs) {
   constexpr int S = 16;
   constexpr int TT = 32 / int(sizeof(T));
-  constexpr int TG = 4;  // tokens whose update loads are issued together
   __shared__ T xt[TT * S * C16_LANES];
+  constexpr int TG = 4;  // tokens whose update loads are issued together
   const int lane = threadIdx.x;
   const int e0 = __builtin_amdgcn_readfirstlane(threadIdx.y) * C16_EPL;
   const int slice = blockIdx.x % nslices, chunk = blockIdx.x / nslices;
