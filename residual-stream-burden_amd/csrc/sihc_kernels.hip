@@ -85,6 +85,9 @@
 #ifndef SIHC_WG_TT  // most tokens per staged LDS tile of the weight / gamma gradients
 #define SIHC_WG_TT 32
 #endif
+#ifndef SIHC_WG_BCG  // most channel-group lanes per weight-gradient block
+#define SIHC_WG_BCG 64
+#endif
 
 #ifndef SIHC_NT  // 1: non-temporal (streaming) hints on carrier/workspace traffic
 #define SIHC_NT 0
@@ -1206,7 +1209,7 @@ int chunk_count(int64_t M, int tokens_per_chunk, int max_chunks) {
 // event lanes (<= 256 threads), `slices` blocks across the channels.
 void wgrad_block(int C, int V, int events, int* bcg_out, int* slices_out) {
   const int CG = (C + V - 1) / V;
-  int bcg = 64;
+  int bcg = SIHC_WG_BCG;
   while (bcg > 1 && bcg * events > 256) bcg /= 2;
   while (bcg > 1 && bcg / 2 >= CG) bcg /= 2;
   *bcg_out = bcg;

@@ -10,6 +10,7 @@ launchers only assert what the C ABI itself needs.
 from __future__ import annotations
 
 import ctypes
+import functools
 from typing import Optional, Sequence
 
 import torch
@@ -25,6 +26,22 @@ def dtype_code(dtype: torch.dtype) -> int:
         return _DTYPES[dtype]
     except KeyError:
         raise ValueError(f"unsupported dtype {dtype}: expected float32 or bfloat16") from None
+
+
+def _on_tensor_device(fn):
+    """Run a launcher with its first tensor argument's GPU as the current HIP device:
+    the library launches on that device's current stream and sizes grids from the
+    current device's properties, which must be the same device."""
+
+    @functools.wraps(fn)
+    def wrapper(*args, **kwargs):
+        dev = next((a.device for a in (*args, *kwargs.values()) if isinstance(a, Tensor) and a.is_cuda), None)
+        if dev is None or dev.index is None or dev.index == torch.cuda.current_device():
+            return fn(*args, **kwargs)
+        with torch.cuda.device(dev):
+            return fn(*args, **kwargs)
+
+    return wrapper
 
 
 def _stream(device: torch.device) -> ctypes.c_void_p:
@@ -47,6 +64,7 @@ def carrier_geometry(x: Tensor, slots: int) -> tuple[int, int, int, int]:
     return b, h // k, k, c
 
 
+@_on_tensor_device
 def read(x: Tensor, alpha: Tensor, index: Optional[Tensor] = None,
          out: Optional[Sequence[Tensor]] = None) -> list[Tensor]:
     """E base reads of carrier x [B,H,W,C] with stacked alpha [E,C,S] (into `out` if given)."""
@@ -60,6 +78,7 @@ def read(x: Tensor, alpha: Tensor, index: Optional[Tensor] = None,
     return out
 
 
+@_on_tensor_device
 def write(x: Tensor, updates: Sequence[Tensor], beta: Tensor, add_x: bool = True,
           index: Optional[Tensor] = None, out: Optional[Tensor] = None) -> Tensor:
     """(add_x ? x : 0) + sum_e beta_e * updates_e written into a new carrier."""
@@ -72,6 +91,7 @@ def write(x: Tensor, updates: Sequence[Tensor], beta: Tensor, add_x: bool = True
     return out
 
 
+@_on_tensor_device
 def weight_grad(x: Tensor, updates: Sequence[Tensor], weights: Optional[Tensor],
                 index: Optional[Tensor] = None, out_dtype: Optional[torch.dtype] = None,
                 slots: Optional[int] = None) -> Tensor:
@@ -92,6 +112,7 @@ def weight_grad(x: Tensor, updates: Sequence[Tensor], weights: Optional[Tensor],
     return out
 
 
+@_on_tensor_device
 def triangular(base: Tensor, updates: Sequence[Tensor], gamma: Tensor) -> Tensor:
     """base + sum_j gamma[j] * updates_j over a [B,N,C] workspace."""
     c = base.shape[-1]
@@ -103,6 +124,7 @@ def triangular(base: Tensor, updates: Sequence[Tensor], gamma: Tensor) -> Tensor
     return out
 
 
+@_on_tensor_device
 def triangular_gamma_grad(grad: Tensor, updates: Sequence[Tensor], gamma: Optional[Tensor],
                           out_dtype: Optional[torch.dtype] = None) -> Tensor:
     """[A,C] (out_dtype, default gamma's dtype) = sum over rows of grad * updates_j."""
@@ -119,6 +141,7 @@ def triangular_gamma_grad(grad: Tensor, updates: Sequence[Tensor], gamma: Option
     return out
 
 
+@_on_tensor_device
 def triangular_backward(grad: Tensor, updates: Sequence[Tensor], gamma: Tensor,
                         out_dtype: Optional[torch.dtype] = None) -> tuple[Tensor, Tensor]:
     """One pass: ([A,B,N,C] stack of grad * gamma[j], [A,C] sum over rows of grad * updates_j).
@@ -140,6 +163,7 @@ def triangular_backward(grad: Tensor, updates: Sequence[Tensor], gamma: Tensor,
     return ddz, dg
 
 
+@_on_tensor_device
 def event_forward(x: Tensor, dz: Tensor, beta: Tensor, alpha_next: Optional[Tensor],
                   index: Optional[Tensor] = None) -> tuple[Tensor, Optional[Tensor]]:
     """x_out = x + beta*dz and z_out = read(x_out, alpha_next) in one pass."""
@@ -152,6 +176,7 @@ def event_forward(x: Tensor, dz: Tensor, beta: Tensor, alpha_next: Optional[Tens
     return x_out, z_out
 
 
+@_on_tensor_device
 def event_backward(grad_x_out: Optional[Tensor], grad_z_out: Optional[Tensor], x_out: Optional[Tensor],
                    dz: Optional[Tensor], beta: Optional[Tensor], alpha_next: Optional[Tensor],
                    index: Optional[Tensor] = None, grad_x: Optional[Tensor] = None,
@@ -183,6 +208,7 @@ def event_backward(grad_x_out: Optional[Tensor], grad_z_out: Optional[Tensor], x
     return grad_x, grad_dz, grad_beta, grad_alpha
 
 
+@_on_tensor_device
 def gather_cells(x: Tensor, index: Optional[Tensor], slots: int) -> Tensor:
     """[B,G*G,S,C] bit-exact copy of each token's cell (cell index[b,n] when given)."""
     b, g, k, c = carrier_geometry(x, slots)
@@ -192,6 +218,7 @@ def gather_cells(x: Tensor, index: Optional[Tensor], slots: int) -> Tensor:
     return cells
 
 
+@_on_tensor_device
 def scatter_cells(cells: Tensor, index: Optional[Tensor], out: Optional[Tensor] = None) -> Tensor:
     """Inverse of gather_cells for a permutation index: new (or `out`) NHWC carrier."""
     b, n, s, c = cells.shape
@@ -204,6 +231,7 @@ def scatter_cells(cells: Tensor, index: Optional[Tensor], out: Optional[Tensor] 
     return out
 
 
+@_on_tensor_device
 def copy_(dst: Tensor, src: Tensor) -> Tensor:
     """Byte copy src -> dst (same number of bytes) with the library's copy kernel."""
     nbytes = src.numel() * src.element_size()
