@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark: SiHC fused read+write, forward + backward, at the SiHC-XL shape.
 
-Workload: batch 256, 16x16 workspace tokens (256 per image), 4
+Workload (benchmark config 2): batch 256, 16x16 workspace tokens (256 per image), 4
 slots per token (32x32 carrier), D = 1152, 28 layers x 2 sublayers = 56 connection
 events, bf16 storage with fp32 accumulation. One step is the whole read/write path of
 one batch: every event's fused write+read forward and its fused backward (carrier,
@@ -65,7 +65,7 @@ def parse_args():
                    help="step: the benchmark (default); calibrate: a 1 GiB copy-kernel launch plus single "
                         "event forward/backward launches at the same shape, for HBM counter runs; kernels: "
                         "every HIP kernel timed alone at the benchmark shape (one JSON line per kernel); e2e: "
-                        "BASELINE config 4, a SiHC-XL denoiser forward on a CFG batch with HIP routing; model: the "
+                        "benchmark config 4, a SiHC-XL denoiser forward on a CFG batch with HIP routing; model: the "
                         "reference's fusion_profile matrix (presets x routing implementation x train/inference)")
     return p.parse_args()
 
@@ -93,7 +93,7 @@ class LiteralStep:
         def randn(shape, mean=0.0, std=1.0):
             return (mean + std * torch.randn(shape, device=dev, generator=g)).to(bf)
 
-        # Draw order: X, alpha, beta, dz, upstream grads (BASELINE config 0/2).
+        # Draw order: X, alpha, beta, dz, upstream grads (the order of benchmark configs 0 and 2).
         self.x = [randn(carrier)] + [torch.empty(carrier, device=dev, dtype=bf) for _ in range(E)]
         self.alpha = torch.stack([randn((S, C), 0.25, 0.02).T.contiguous() for _ in range(E)])  # [E,C,S]
         self.beta = torch.stack([randn((S, C), 1.0, 0.02).T.contiguous() for _ in range(E)])
@@ -185,7 +185,7 @@ def _timed(torch, fn, iters=10, warmup=2):
 
 
 def extra_configs(seed: int) -> dict:
-    """Secondary figures on BASELINE configs 1 and 3 (not the headline `value`).
+    """Secondary figures on benchmark configs 1 and 3 (not the headline `value`).
 
     config 1: SiHC-B shape (batch 256, D=768), forward only, one 24-event stage, as the
       per-event fused schedule and as the reference's stage API (read E=24, triangular
@@ -295,7 +295,7 @@ def extra_configs(seed: int) -> dict:
 
 
 def cpu_baseline(budget_s: float) -> dict:
-    """BASELINE config 0 on the host: the oracle's unfused PyTorch read/write (fp32,
+    """benchmark config 0 on the host: the oracle's unfused PyTorch read/write (fp32,
     batch 8, 256 tokens, 4 slots, D=768, one event) forward + autograd backward."""
     import torch
 
@@ -337,7 +337,7 @@ def cpu_baseline(budget_s: float) -> dict:
         "tokens_per_s": round(8 * 256 / t, 1),
         "fwd_ms": round(statistics.median(fwd) * 1e3, 3), "bwd_ms": round(statistics.median(bwd) * 1e3, 3),
         "runs": len(fwd),
-        "sample": ("BASELINE config 0 on the host: oracle/ restatement of the reference's unfused PyTorch "
+        "sample": ("benchmark config 0 on the host: oracle/ restatement of the reference's unfused PyTorch "
                    "read_torch/write_torch + autograd, fp32, batch 8 x 256 tokens, 4 slots, D=768, one event "
                    "fwd+bwd, median of up to 20 runs after 3 warmups; GB/s from the same algorithmic bytes "
                    "(14 U fwd + 20 U bwd, U = one fp32 workspace tensor)"),
@@ -460,7 +460,7 @@ def kernels(args) -> None:
 
 
 def e2e_config4(seed: int, schedules=("stage", "literal"), steps: int = 5) -> dict:
-    """SiHC-XL sublayer denoiser (p8, D=1152, 28 blocks, 16 heads,
+    """benchmark config 4: SiHC-XL sublayer denoiser (p8, D=1152, 28 blocks, 16 heads,
     MLP ratio 4, stages 8/12/8), bf16, random init; one forward of 64 class-conditional
     + 64 unconditional (label 1000) samples from N(0,1) images, t ~ U(0,1). Routing on
     the HIP ops; bodies on PyTorch-ROCm. Reports samples/s, images/s per CFG step and
@@ -475,7 +475,7 @@ def e2e_config4(seed: int, schedules=("stage", "literal"), steps: int = 5) -> di
     x = torch.randn(128, 3, 256, 256, device=dev).to(torch.bfloat16)
     t = torch.rand(128, device=dev)
     y = torch.cat([torch.randint(0, 1000, (64,), device=dev), torch.full((64,), 1000, device=dev)])
-    out = {"workload": "BASELINE config 4: SiHC-XL sublayer denoiser forward, CFG batch 64+64, bf16, random init"}
+    out = {"workload": "benchmark config 4: SiHC-XL sublayer denoiser forward, CFG batch 64+64, bf16, random init"}
     for schedule in schedules:
         model.schedule = schedule
         with torch.no_grad():
@@ -726,7 +726,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "BASELINE config 2: SiHC-XL-shape fused read/write fwd+bwd, literal per-event schedule",
+            "workload": "benchmark config 2: SiHC-XL-shape fused read/write fwd+bwd, literal per-event schedule",
             "batch": args.batch, "tokens": 256, "slots": 4, "channels": args.channels,
             "events": args.events, "schedule": "per-event fused (write+read, one carrier pass per event)",
             "parallelism": "single GPU",

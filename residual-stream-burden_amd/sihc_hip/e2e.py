@@ -1,4 +1,4 @@
-"""Compact SiHC sublayer denoiser whose routing runs on the HIP ops.
+"""Compact SiHC sublayer denoiser whose routing runs on the HIP ops (benchmark config 4).
 
 Architecture (behaviour of tongtongliang/residual-stream-burden
 sihc/models/sihc/sublayer.py:30-128, model.py:186-682 and components.py:14-324):

@@ -1,4 +1,4 @@
-"""GPU checks at BASELINE's full workload sizes.
+"""GPU checks at the full sizes of the benchmark configurations (0-4).
 
 The kernels treat tokens independently, so per-token outputs are checked on batch
 slices against the CPU oracle; token reductions (weight gradients) are checked

@@ -210,7 +210,7 @@ def test_fp32_carrier_with_bf16_updates_chained_writes():
 
 
 def test_baseline_config0_single_event_fp32():
-    # B8, 256 tokens, 4 slots, D=768, fp32; alpha ~ N(0.25,0.02),
+    # benchmark config 0: B8, 256 tokens, 4 slots, D=768, fp32; alpha ~ N(0.25,0.02),
     # beta ~ N(1,0.02) drawn [S,C] and passed [C,S]; loss <gX', X'> + <gz, z>.
     announce("config0 fp32 one event fwd+bwd")
     torch.manual_seed(0)
