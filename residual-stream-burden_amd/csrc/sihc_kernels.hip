@@ -1446,9 +1446,12 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
   int bcg, slices;
   wgrad_block(g.C, V, events, &bcg, &slices);
   const int tpb = int((int64_t(g.M) + chunks - 1) / chunks);
-  // x tile of TT tokens: at most 32 KB of LDS.
+  // x tile of TT tokens: at most 32 KB of LDS. With 16 or fewer event lanes on the
+  // carrier, 8-token tiles keep one round of update loads per tile (measured: E=16
+  // 828 -> 766 us at the XL shape; more events or the workspace mode prefer 32). The
+  // tile size does not change the summation order.
   int tt = 32768 / (S * bcg * V * int(sizeof(float)));
-  tt = std::max(1, std::min(tt, SIHC_WG_TT));
+  tt = std::max(1, std::min(tt, carrier && events <= 16 ? 8 : SIHC_WG_TT));
   const size_t lds = size_t(tt) * S * bcg * V * sizeof(float);
   const PtrPack pk = pack(z, events);
   const PtrPack dk = dout ? pack(const_cast<const void* const*>(dout), events) : PtrPack{};
