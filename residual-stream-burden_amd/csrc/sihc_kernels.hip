@@ -101,6 +101,9 @@
 #ifndef SIHC_RW_MINW  // minimum waves per SIMD read / write are compiled for (caps VGPRs)
 #define SIHC_RW_MINW 3
 #endif
+#ifndef SIHC_C16Z  // 1: pipelined 16-slot weight gradient (k_wgrad16z) where it applies
+#define SIHC_C16Z 1
+#endif
 #ifndef SIHC_XCD_MAP  // 1: XCD-contiguous logical block order (see logical_block)
 #define SIHC_XCD_MAP 1
 #endif
@@ -816,6 +819,121 @@ __global__ void __launch_bounds__(512) k_wgrad16(const T* __restrict__ x, PtrPac
   }
 }
 
+// Pipelined 16-slot weight gradient for bf16 rows of whole 16-byte vectors and 8+
+// events. The update rows join the carrier tile in LDS (16-byte loads: each wave stages
+// whole 64-channel rows of its own events, so the update pointer stays wave-uniform),
+// and the loads of tile k+1 are issued into registers before tile k is reduced, so
+// every tile's HBM latency overlaps the previous tile's arithmetic. Tokens are summed
+// in the same ascending order as k_wgrad16: the partial rows are identical bit for bit.
+// NXQ = carrier vectors staged per thread (1024 / threads, rounded up); EPL = events
+// per lane (4, or 3 where that makes the wave count a multiple of 4: the 4 SIMDs
+// of a CU then hold equal shares of each block; E = 24 with 6 waves: 2031 us, with 8
+// waves of 3 events: 1528 us at batch 256, D 1152).
+#ifndef SIHC_C16Z_MINW  // minimum waves per SIMD k_wgrad16z is compiled for
+#define SIHC_C16Z_MINW 1
+#endif
+#ifndef SIHC_C16Z_TT
+#define SIHC_C16Z_TT 8  // tokens per tile; TT * (64 / 8) must equal one wave (64 lanes)
+#endif
+template <int NXQ, int EPL>
+__global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgrad16z(const bf16_t* __restrict__ x, PtrPack z, float* __restrict__ part,
+                                                  const int32_t* __restrict__ index, int E, Geo g, int tpb,
+                                                  int nslices) {
+  constexpr int S = 16, TT = SIHC_C16Z_TT, VS = 8, NV = C16_LANES / VS;
+  constexpr int NXV = TT * S * NV;  // carrier vectors per tile
+  constexpr int NZQ = EPL;  // update rows (events) staged per wave: ceil(E / ceil(E / EPL)) <= EPL
+  static_assert(TT * NV == C16_LANES, "a wave stages one event's TT update rows");
+  using R = u32x4;
+  extern __shared__ __align__(16) unsigned char smem16[];
+  bf16_t* xt = reinterpret_cast<bf16_t*>(smem16);  // [TT][S][64]
+  bf16_t* zt = xt + TT * S * C16_LANES;            // [TT][E][64]
+  const int lane = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.y);
+  const int nw = blockDim.y, nthr = C16_LANES * nw, tid = wave * C16_LANES + lane;
+  const int e0 = wave * EPL;
+  const int blk = logical_block<false>(), slice = blk % nslices, chunk = blk / nslices;
+  const int cs = slice * C16_LANES, c = cs + lane;
+  const bool cok = c < g.C;
+  // this lane's update row slot: token zt_t, vector zt_j of the 64-channel row
+  const int zt_t = lane / NV, zt_j = lane % NV, zc = cs + zt_j * VS;
+  R xb[NXQ], zb[NZQ];
+  // Every load is issued, at a clamped in-range address where its vector is not part
+  // of the tile (commit skips those): no branches between the loads, so they all stay
+  // in flight together. Addresses (and index reads) are formed before the first load.
+  auto issue = [&](int t0, int tn) {
+    int64_t off[NXQ];
+#pragma unroll
+    for (int k = 0; k < NXQ; ++k) {
+      const int i = min(tid + k * nthr, NXV - 1);
+      const int row = i / NV, t = min(row / S, tn - 1), cc = cs + (i % NV) * VS;
+      off[k] = slot_offset<4>(cell_pixel0(t0 + t, g, index), row % S, g, cc < g.C ? cc : cs);
+    }
+    const int64_t zoff = int64_t(t0 + min(zt_t, tn - 1)) * g.C + (zc < g.C ? zc : cs);
+#pragma unroll
+    for (int k = 0; k < NXQ; ++k) xb[k] = ld(reinterpret_cast<const R*>(x + off[k]));
+#pragma unroll
+    for (int k = 0; k < NZQ; ++k) {
+      const int e = min(wave + k * nw, E - 1);
+      zb[k] = ld(reinterpret_cast<const R*>(static_cast<const bf16_t*>(z.p[e]) + zoff));
+    }
+  };
+  auto commit = [&](int tn) {
+#pragma unroll
+    for (int k = 0; k < NXQ; ++k) {
+      const int i = tid + k * nthr;
+      const int row = i / NV, t = row / S, cc = cs + (i % NV) * VS;
+      if (i < NXV && t < tn && cc < g.C) *reinterpret_cast<R*>(xt + row * C16_LANES + (i % NV) * VS) = xb[k];
+    }
+#pragma unroll
+    for (int k = 0; k < NZQ; ++k) {
+      const int e = wave + k * nw;
+      if (e < E && zt_t < tn && zc < g.C)
+        *reinterpret_cast<R*>(zt + (zt_t * E + e) * C16_LANES + zt_j * VS) = zb[k];
+    }
+  };
+  int zrow[EPL];  // this lane's event rows within a token's update rows (clamped)
+#pragma unroll
+  for (int q = 0; q < EPL; ++q) zrow[q] = min(e0 + q, E - 1);
+  float acc[EPL][S];
+#pragma unroll
+  for (int q = 0; q < EPL; ++q)
+#pragma unroll
+    for (int s = 0; s < S; ++s) acc[q][s] = 0.f;
+  const int m_begin = chunk * tpb;
+  const int m_end = min(m_begin + tpb, g.M);
+  if (m_begin < m_end) issue(m_begin, min(TT, m_end - m_begin));
+  for (int t0 = m_begin; t0 < m_end; t0 += TT) {
+    const int tn = min(TT, m_end - t0);
+    __syncthreads();  // the previous tile is fully reduced
+    commit(tn);
+    __syncthreads();
+    if (t0 + TT < m_end) issue(t0 + TT, min(TT, m_end - t0 - TT));
+    load_fence();
+    if (cok) {
+      for (int t = 0; t < tn; ++t) {
+        float zv[EPL];
+#pragma unroll
+        for (int q = 0; q < EPL; ++q) zv[q] = to_f32(zt[(t * E + zrow[q]) * C16_LANES + lane]);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const float xs = to_f32(xt[(t * S + s) * C16_LANES + lane]);
+#pragma unroll
+          for (int q = 0; q < EPL; ++q) acc[q][s] = fmaf(xs, zv[q], acc[q][s]);
+        }
+      }
+    }
+  }
+  if (!cok) return;
+#pragma unroll
+  for (int q = 0; q < EPL; ++q) {
+    if (e0 + q < E) {
+      float* prow = part + (int64_t(chunk) * E + e0 + q) * S * g.C + c;
+#pragma unroll
+      for (int s = 0; s < S; ++s) prow[int64_t(s) * g.C] = acc[q][s];
+    }
+  }
+}
+
 // ----------------------------------------------------------------------------------
 // Fixed-order sum of partial rows. part is [chunks][R][S][C]; row r of the result
 // goes to out0 + r*C*S ([R][C][S], `pair` == 0) or, with `pair`, row 0 -> out0 and
@@ -1464,8 +1582,9 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
                  int S, bool carrier, const int32_t* index, int dtype, int out_dtype, void* workspace,
                  size_t workspace_bytes, hipStream_t st, void* const* dout = nullptr, const void* gamma = nullptr,
                  int gamma_dtype = SIHC_DTYPE_F32) {
-  const int chunks = wgrad_chunks(g.M, events, g.C);
-  const size_t need = size_t(chunks) * events * S * g.C * sizeof(float);
+  const int max_chunks = wgrad_chunks(g.M, events, g.C);
+  int chunks = max_chunks;  // k_wgrad16z may use fewer (whole rounds of resident blocks)
+  const size_t need = size_t(max_chunks) * events * S * g.C * sizeof(float);
   if (!workspace || workspace_bytes < need)
     return fail(SIHC_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", what, need, workspace_bytes);
   if (!aligned(workspace, 16)) return fail(SIHC_ERR_INVALID, "%s: workspace must be 16-byte aligned", what);
@@ -1492,6 +1611,10 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
   // 16-slot carrier: k_wgrad16 (one channel per lane); only x is loaded as vectors
   const int slices16 = (g.C + C16_LANES - 1) / C16_LANES;
   const int vs16 = pick_vec(g.C, es, 8, &x, 1);
+  // pipelined k_wgrad16z: bf16, 8+ events, every row of x and the updates in whole
+  // 16-byte vectors (C % 8 == 0, 16-byte aligned pointers)
+  const bool use16z = SIHC_C16Z && dtype == SIHC_DTYPE_BF16 && events >= 8 && events <= 24 && !dout &&
+                      pick_vec(g.C, es, 8, ptrs, nptr) == 8;
   float* part = static_cast<float*>(workspace);
   const int gf32 = gamma_dtype == SIHC_DTYPE_F32;
   int rc = with_dtype(dtype, [&](auto t) {
@@ -1506,9 +1629,50 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
           constexpr bool CAR = decltype(car)::value;
           constexpr bool SD = decltype(sd)::value;
           if constexpr (CAR && KK == 4) {
-            hipLaunchKernelGGL((k_wgrad16<T>), dim3(blocks1d(slices16, chunks)),
-                               dim3(C16_LANES, (events + C16_EPL - 1) / C16_EPL), 0, st, static_cast<const T*>(x), pk,
-                               part, index, events, g, tpb, slices16, vs16);
+            if (std::is_same<T, bf16_t>::value && use16z) {
+              const size_t lds16 = size_t(SIHC_C16Z_TT) * (16 + events) * C16_LANES * sizeof(bf16_t);
+              // events per lane: 4, or 3 where only that makes the wave count a multiple
+              // of 4 (at most 8 waves)
+              int epl = 4;
+              for (int ep : {4, 3}) {
+                const int w = (events + ep - 1) / ep;
+                if (w % 4 == 0 && w <= 8) {
+                  epl = ep;
+                  break;
+                }
+              }
+              const int nw = (events + epl - 1) / epl;
+              auto go16z = [&](auto nq, auto epl) {
+                constexpr int NQ = decltype(nq)::value;
+                constexpr int EP = decltype(epl)::value;
+                // 2-4 blocks per CU: size the grid to whole rounds of resident blocks so
+                // the last round is not left partly empty (e.g. E = 24: 4.5 -> 4 rounds)
+                const void* kfn = reinterpret_cast<const void*>(&k_wgrad16z<NQ, EP>);
+                chunks = whole_rounds(slices16, max_chunks, resident_blocks(kfn, C16_LANES * nw, lds16));
+                const int tpb16 = int((int64_t(g.M) + chunks - 1) / chunks);
+                hipLaunchKernelGGL((k_wgrad16z<NQ, EP>), dim3(blocks1d(slices16, chunks)), dim3(C16_LANES, nw), lds16,
+                                   st, static_cast<const bf16_t*>(x), pk, part, index, events, g, tpb16, slices16);
+              };
+              // carrier vectors per thread: 1024 / (64 * nw), rounded up
+              if (epl == 3) {
+                if (nw == 4) go16z(IC<4>{}, IC<3>{});
+                else go16z(IC<2>{}, IC<3>{});  // nw = 8
+              } else if (nw == 2) {
+                go16z(IC<8>{}, IC<4>{});
+              } else if (nw == 3) {
+                go16z(IC<6>{}, IC<4>{});
+              } else if (nw <= 5) {
+                go16z(IC<4>{}, IC<4>{});
+              } else if (nw <= 7) {
+                go16z(IC<3>{}, IC<4>{});
+              } else {
+                go16z(IC<2>{}, IC<4>{});
+              }
+            } else {
+              const int nw = (events + C16_EPL - 1) / C16_EPL;
+              hipLaunchKernelGGL((k_wgrad16<T>), dim3(blocks1d(slices16, chunks)), dim3(C16_LANES, nw), 0, st,
+                                 static_cast<const T*>(x), pk, part, index, events, g, tpb, slices16, vs16);
+            }
           } else {
             if (events <= 2) {
               hipLaunchKernelGGL((k_wgrad_direct<T, VV, KK, CAR, SD>), dim3(blocks1d(slices, chunks)),
