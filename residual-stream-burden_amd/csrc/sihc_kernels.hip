@@ -819,27 +819,33 @@ __global__ void __launch_bounds__(512) k_wgrad16(const T* __restrict__ x, PtrPac
   }
 }
 
-// Pipelined 16-slot weight gradient for bf16 rows of whole 16-byte vectors and 8+
-// events. The update rows join the carrier tile in LDS (16-byte loads: each wave stages
-// whole 64-channel rows of its own events, so the update pointer stays wave-uniform),
-// and the loads of tile k+1 are issued into registers before tile k is reduced, so
-// every tile's HBM latency overlaps the previous tile's arithmetic. Tokens are summed
-// in the same ascending order as k_wgrad16: the partial rows are identical bit for bit.
-// NXQ = carrier vectors staged per thread (1024 / threads, rounded up); EPL = events
-// per lane (4, or 3 where that makes the wave count a multiple of 4: the 4 SIMDs
-// of a CU then hold equal shares of each block; E = 24 with 6 waves: 2031 us, with 8
-// waves of 3 events: 1528 us at batch 256, D 1152).
-#ifndef SIHC_C16Z_MINW  // minimum waves per SIMD k_wgrad16z is compiled for
+// Pipelined carrier weight gradient (4- and 16-slot cells) for bf16 rows of whole
+// 16-byte vectors and 8+ events. A lane owns ONE channel and EPL events (EPL x S
+// accumulators). The update rows join the carrier tile in LDS (16-byte loads: each wave
+// stages whole 64-channel rows of its own events, so the update pointer stays
+// wave-uniform), and the loads of tile k+1 are issued into registers before tile k is
+// reduced, so every tile's HBM latency overlaps the previous tile's arithmetic. Tokens
+// are summed in ascending order, as in k_wgrad16 and k_wgrad: for the same chunks the
+// partial rows are identical bit for bit.
+// NXQ = carrier vectors staged per thread (TT * S * 8 / threads, rounded up); EPL is
+// chosen so that the wave count is a multiple of 4 where possible: the 4 SIMDs of a CU
+// then hold equal shares of each block (16 slots, E = 24: 6 waves of 4 events 2031 us,
+// 8 waves of 3 events 1528 us at batch 256, D 1152).
+#ifndef SIHC_WGZ_K2  // 1: 4-slot carriers also use k_wgradz where its waves balance
+#define SIHC_WGZ_K2 1
+#endif
+#ifndef SIHC_C16Z_MINW  // minimum waves per SIMD k_wgradz is compiled for
 #define SIHC_C16Z_MINW 1
 #endif
 #ifndef SIHC_C16Z_TT
 #define SIHC_C16Z_TT 8  // tokens per tile; TT * (64 / 8) must equal one wave (64 lanes)
 #endif
-template <int NXQ, int EPL>
-__global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgrad16z(const bf16_t* __restrict__ x, PtrPack z, float* __restrict__ part,
-                                                  const int32_t* __restrict__ index, int E, Geo g, int tpb,
-                                                  int nslices) {
-  constexpr int S = 16, TT = SIHC_C16Z_TT, VS = 8, NV = C16_LANES / VS;
+template <int K, int NXQ, int EPL>
+__global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgradz(const bf16_t* __restrict__ x, PtrPack z,
+                                                                float* __restrict__ part,
+                                                                const int32_t* __restrict__ index, int E, Geo g,
+                                                                int tpb, int nslices) {
+  constexpr int S = K * K, TT = SIHC_C16Z_TT, VS = 8, NV = C16_LANES / VS;
   constexpr int NXV = TT * S * NV;  // carrier vectors per tile
   constexpr int NZQ = EPL;  // update rows (events) staged per wave: ceil(E / ceil(E / EPL)) <= EPL
   static_assert(TT * NV == C16_LANES, "a wave stages one event's TT update rows");
@@ -866,7 +872,7 @@ __global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgrad16z(const bf16_t* 
     for (int k = 0; k < NXQ; ++k) {
       const int i = min(tid + k * nthr, NXV - 1);
       const int row = i / NV, t = min(row / S, tn - 1), cc = cs + (i % NV) * VS;
-      off[k] = slot_offset<4>(cell_pixel0(t0 + t, g, index), row % S, g, cc < g.C ? cc : cs);
+      off[k] = slot_offset<K>(cell_pixel0(t0 + t, g, index), row % S, g, cc < g.C ? cc : cs);
     }
     const int64_t zoff = int64_t(t0 + min(zt_t, tn - 1)) * g.C + (zc < g.C ? zc : cs);
 #pragma unroll
@@ -1611,10 +1617,11 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
   // 16-slot carrier: k_wgrad16 (one channel per lane); only x is loaded as vectors
   const int slices16 = (g.C + C16_LANES - 1) / C16_LANES;
   const int vs16 = pick_vec(g.C, es, 8, &x, 1);
-  // pipelined k_wgrad16z: bf16, 8+ events, every row of x and the updates in whole
+  // pipelined k_wgradz: bf16, 8..24 events, every row of x and the updates in whole
   // 16-byte vectors (C % 8 == 0, 16-byte aligned pointers)
-  const bool use16z = SIHC_C16Z && dtype == SIHC_DTYPE_BF16 && events >= 8 && events <= 24 && !dout &&
-                      pick_vec(g.C, es, 8, ptrs, nptr) == 8;
+  const bool usez = SIHC_C16Z && dtype == SIHC_DTYPE_BF16 && events >= 8 && events <= 24 && !dout &&
+                    pick_vec(g.C, es, 8, ptrs, nptr) == 8;
+  const int slicesz = (g.C + C16_LANES - 1) / C16_LANES;
   float* part = static_cast<float*>(workspace);
   const int gf32 = gamma_dtype == SIHC_DTYPE_F32;
   int rc = with_dtype(dtype, [&](auto t) {
@@ -1628,51 +1635,54 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
           constexpr int KK = decltype(kk)::value;
           constexpr bool CAR = decltype(car)::value;
           constexpr bool SD = decltype(sd)::value;
+          // pipelined k_wgradz<KZ, NQ, EP> with nw event waves
+          auto goz = [&](auto kz, auto nq, auto ep, int nw) {
+            constexpr int KZ = decltype(kz)::value;
+            constexpr int NQ = decltype(nq)::value;
+            constexpr int EP = decltype(ep)::value;
+            const size_t ldsz = size_t(SIHC_C16Z_TT) * (KZ * KZ + events) * C16_LANES * sizeof(bf16_t);
+            // whole rounds of resident blocks, so the last round is not part-empty
+            const void* kfn = reinterpret_cast<const void*>(&k_wgradz<KZ, NQ, EP>);
+            chunks = whole_rounds(slicesz, max_chunks, resident_blocks(kfn, C16_LANES * nw, ldsz));
+            const int tpbz = int((int64_t(g.M) + chunks - 1) / chunks);
+            hipLaunchKernelGGL((k_wgradz<KZ, NQ, EP>), dim3(blocks1d(slicesz, chunks)), dim3(C16_LANES, nw), ldsz, st,
+                               reinterpret_cast<const bf16_t*>(x), pk, part, index, events, g, tpbz, slicesz);
+          };
+          // events per lane: the first candidate giving 4 or 8 event waves (0: none)
+          auto balanced_epl = [&](std::initializer_list<int> cands) {
+            for (int ep : cands)
+              if ((events + ep - 1) / ep == 4 || (events + ep - 1) / ep == 8) return ep;
+            return 0;
+          };
+          const bool bf = std::is_same<T, bf16_t>::value && usez;
           if constexpr (CAR && KK == 4) {
-            if (std::is_same<T, bf16_t>::value && use16z) {
-              const size_t lds16 = size_t(SIHC_C16Z_TT) * (16 + events) * C16_LANES * sizeof(bf16_t);
-              // events per lane: 4, or 3 where only that makes the wave count a multiple
-              // of 4 (at most 8 waves)
-              int epl = 4;
-              for (int ep : {4, 3}) {
-                const int w = (events + ep - 1) / ep;
-                if (w % 4 == 0 && w <= 8) {
-                  epl = ep;
-                  break;
-                }
-              }
-              const int nw = (events + epl - 1) / epl;
-              auto go16z = [&](auto nq, auto epl) {
-                constexpr int NQ = decltype(nq)::value;
-                constexpr int EP = decltype(epl)::value;
-                // 2-4 blocks per CU: size the grid to whole rounds of resident blocks so
-                // the last round is not left partly empty (e.g. E = 24: 4.5 -> 4 rounds)
-                const void* kfn = reinterpret_cast<const void*>(&k_wgrad16z<NQ, EP>);
-                chunks = whole_rounds(slices16, max_chunks, resident_blocks(kfn, C16_LANES * nw, lds16));
-                const int tpb16 = int((int64_t(g.M) + chunks - 1) / chunks);
-                hipLaunchKernelGGL((k_wgrad16z<NQ, EP>), dim3(blocks1d(slices16, chunks)), dim3(C16_LANES, nw), lds16,
-                                   st, static_cast<const bf16_t*>(x), pk, part, index, events, g, tpb16, slices16);
-              };
-              // carrier vectors per thread: 1024 / (64 * nw), rounded up
-              if (epl == 3) {
-                if (nw == 4) go16z(IC<4>{}, IC<3>{});
-                else go16z(IC<2>{}, IC<3>{});  // nw = 8
-              } else if (nw == 2) {
-                go16z(IC<8>{}, IC<4>{});
-              } else if (nw == 3) {
-                go16z(IC<6>{}, IC<4>{});
-              } else if (nw <= 5) {
-                go16z(IC<4>{}, IC<4>{});
-              } else if (nw <= 7) {
-                go16z(IC<3>{}, IC<4>{});
+            if (bf) {
+              // 16 slots: 3 events per lane where that balances the SIMDs, else 4 with
+              // 2..8 waves; carrier vectors per thread = 1024 / (64 * waves), rounded up
+              if (balanced_epl({4, 3}) == 3) {
+                const int nw = (events + 2) / 3;
+                if (nw == 4) goz(IC<4>{}, IC<4>{}, IC<3>{}, nw);
+                else goz(IC<4>{}, IC<2>{}, IC<3>{}, nw);
               } else {
-                go16z(IC<2>{}, IC<4>{});
+                const int nw = (events + 3) / 4;
+                if (nw == 2) goz(IC<4>{}, IC<8>{}, IC<4>{}, nw);
+                else if (nw == 3) goz(IC<4>{}, IC<6>{}, IC<4>{}, nw);
+                else if (nw <= 5) goz(IC<4>{}, IC<4>{}, IC<4>{}, nw);
+                else if (nw <= 7) goz(IC<4>{}, IC<3>{}, IC<4>{}, nw);
+                else goz(IC<4>{}, IC<2>{}, IC<4>{}, nw);
               }
             } else {
               const int nw = (events + C16_EPL - 1) / C16_EPL;
               hipLaunchKernelGGL((k_wgrad16<T>), dim3(blocks1d(slices16, chunks)), dim3(C16_LANES, nw), 0, st,
                                  static_cast<const T*>(x), pk, part, index, events, g, tpb, slices16, vs16);
             }
+          } else if (CAR && KK == 2 && bf && SIHC_WGZ_K2 && balanced_epl({6, 4, 3, 2})) {
+            // 4 slots, only where the waves balance (4 or 8 waves: 1 carrier vector each)
+            const int ep = balanced_epl({6, 4, 3, 2}), nw = (events + ep - 1) / ep;
+            if (ep == 6) goz(IC<2>{}, IC<1>{}, IC<6>{}, nw);
+            else if (ep == 4) goz(IC<2>{}, IC<1>{}, IC<4>{}, nw);
+            else if (ep == 3) goz(IC<2>{}, IC<1>{}, IC<3>{}, nw);
+            else goz(IC<2>{}, IC<1>{}, IC<2>{}, nw);
           } else {
             if (events <= 2) {
               hipLaunchKernelGGL((k_wgrad_direct<T, VV, KK, CAR, SD>), dim3(blocks1d(slices, chunks)),
