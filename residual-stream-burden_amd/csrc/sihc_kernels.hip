@@ -1,8 +1,9 @@
 // SiHC hyper-connection read/write path for MI355X (gfx950, CDNA4, wave64).
 //
-// All kernels here are HBM-bound weighted stream reductions and broadcasts over a
-// packed NHWC carrier and packed [tokens, channels] workspace tensors. There is no
-// matrix-core work: per element the path does at most 2*E*S flops per 2*(S+E) bytes.
+// All kernels here are weighted stream reductions and broadcasts over a packed NHWC
+// carrier and packed [tokens, channels] workspace tensors, HBM-bound at 4-slot cells.
+// There is no matrix-core work: per element the path does at most 2*E*S flops per
+// 2*(S+E) bytes.
 //
 // Thread mapping shared by every kernel: a block is (BCG channel groups) x (TL token
 // lanes). A lane owns V adjacent channels (up to one 16-byte vector) and walks a run of
@@ -101,7 +102,7 @@
 #ifndef SIHC_RW_MINW  // minimum waves per SIMD read / write are compiled for (caps VGPRs)
 #define SIHC_RW_MINW 3
 #endif
-#ifndef SIHC_C16Z  // 1: pipelined 16-slot weight gradient (k_wgrad16z) where it applies
+#ifndef SIHC_C16Z  // 1: pipelined carrier weight gradient (k_wgradz) where it applies
 #define SIHC_C16Z 1
 #endif
 #ifndef SIHC_XCD_MAP  // 1: XCD-contiguous logical block order (see logical_block)
@@ -1589,7 +1590,7 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
                  size_t workspace_bytes, hipStream_t st, void* const* dout = nullptr, const void* gamma = nullptr,
                  int gamma_dtype = SIHC_DTYPE_F32) {
   const int max_chunks = wgrad_chunks(g.M, events, g.C);
-  int chunks = max_chunks;  // k_wgrad16z may use fewer (whole rounds of resident blocks)
+  int chunks = max_chunks;  // k_wgradz may use fewer (whole rounds of resident blocks)
   const size_t need = size_t(max_chunks) * events * S * g.C * sizeof(float);
   if (!workspace || workspace_bytes < need)
     return fail(SIHC_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", what, need, workspace_bytes);
