@@ -5,8 +5,8 @@ kernel (one channel per lane, EPL events per lane, 2..8 event waves); other even
 counts, channel counts that are not multiples of 8 and fp32 take the other kernels.
 Products of bf16 values are exact in fp32 and the sums are fp32, so the fp32 bar applies
 against the oracle's float64 sums of the same bf16 inputs. Token tails (grids of 5x5
-cells), channel tails (136 = 2 x 64 + 8 channels) and per-batch state permutations are
-covered.
+cells), channel tails (136 = 2 x 64 + 8 channels; 24 channels in one 64-lane slice) and
+per-batch state permutations are covered.
 """
 from __future__ import annotations
 
@@ -38,11 +38,11 @@ CASES = [
     (16, 24),  # 3 x 8
     (16, 25),  # the one-channel-per-lane kernel
 ]
-GEOMS = [(2, 16, 64, False), (3, 5, 136, True), (1, 16, 1152, True)]
+GEOMS = [(2, 16, 64, False), (3, 5, 136, True), (1, 16, 1152, True), (2, 4, 24, False)]
 
 
 @pytest.mark.parametrize("slots,events", CASES, ids=[f"s{s}-e{e}" for s, e in CASES])
-@pytest.mark.parametrize("geom", GEOMS, ids=["b2-g16-c64", "b3-g5-c136-index", "b1-g16-c1152-index"])
+@pytest.mark.parametrize("geom", GEOMS, ids=["b2-g16-c64", "b3-g5-c136-index", "b1-g16-c1152-index", "b2-g4-c24"])
 def test_carrier_weight_grad_bf16(slots, events, geom):
     b, g, c, with_index = geom
     k = O.cell_edge(slots)
