@@ -184,6 +184,22 @@ def _timed(torch, fn, iters=10, warmup=2):
     return a.elapsed_time(b) / iters * 1e-3
 
 
+def copy_ceiling() -> dict:
+    """The library's 16-byte grid-stride copy of 1 GiB on the same GPU in the same run:
+    a plain 1:1 read/write stream, the context for the per-event kernels' fraction of
+    the nominal 8 TB/s (the per-event backward moves 10 units read : 5 written)."""
+    import torch
+
+    from sihc_hip import launch
+
+    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    sec = _timed(torch, lambda: launch.copy_(dst, src), iters=20, warmup=3)
+    gbs = 2 * src.numel() / sec / 1e9
+    return {"workload": "1 GiB copy (1 GiB read + 1 GiB written), 16-byte vectors", "ms": round(sec * 1e3, 3),
+            "GB/s": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def extra_configs(seed: int) -> dict:
     """Secondary figures on benchmark configs 1 and 3 (not the headline `value`).
 
@@ -754,6 +770,7 @@ def main():
         torch.cuda.empty_cache()
         print("[bench] secondary configs 1 and 3", file=sys.stderr, flush=True)
         result["extra"] = extra_configs(args.seed)
+        result["extra"]["copy_ceiling"] = copy_ceiling()
         torch.cuda.empty_cache()
         print("[bench] config 4 end-to-end forward", file=sys.stderr, flush=True)
         result["extra"]["config4_e2e"] = e2e_config4(args.seed)
