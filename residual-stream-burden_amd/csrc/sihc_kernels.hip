@@ -105,6 +105,9 @@
 #ifndef SIHC_C16Z  // 1: pipelined carrier weight gradient (k_wgradz) where it applies
 #define SIHC_C16Z 1
 #endif
+#ifndef SIHC_WR_PF  // 1: k_write prefetches the next event group's update rows
+#define SIHC_WR_PF 1
+#endif
 #ifndef SIHC_XCD_MAP  // 1: XCD-contiguous logical block order (see logical_block)
 #define SIHC_XCD_MAP 1
 #endif
@@ -229,6 +232,34 @@ __device__ __forceinline__ void load_vec_cached(const T* __restrict__ p, float* 
     R r = reinterpret_cast<const R*>(p)[q];
     T e[EPC];
     __builtin_memcpy(e, &r, CH);
+#pragma unroll
+    for (int i = 0; i < EPC; ++i) o[q * EPC + i] = to_f32(e[i]);
+  }
+}
+
+// V elements of T as the raw words a vector load returns: loaded now, converted later
+// (a prefetch held in registers costs half the VGPRs of its fp32 values for bf16).
+template <typename T, int V>
+struct RawVec {
+  static constexpr int BYTES = V * int(sizeof(T));
+  static constexpr int CH = BYTES >= 16 ? 16 : BYTES;
+  using R = typename RawT<CH>::type;
+  R r[BYTES / CH];
+};
+template <typename T, int V>
+__device__ __forceinline__ void load_raw(const T* __restrict__ p, RawVec<T, V>& o) {
+  using RV = RawVec<T, V>;
+#pragma unroll
+  for (int q = 0; q < RV::BYTES / RV::CH; ++q) o.r[q] = ld(reinterpret_cast<const typename RV::R*>(p) + q);
+}
+template <typename T, int V>
+__device__ __forceinline__ void raw_to_f32(const RawVec<T, V>& in, float* o) {
+  using RV = RawVec<T, V>;
+  constexpr int EPC = RV::CH / int(sizeof(T));
+#pragma unroll
+  for (int q = 0; q < RV::BYTES / RV::CH; ++q) {
+    T e[EPC];
+    __builtin_memcpy(e, &in.r[q], RV::CH);
 #pragma unroll
     for (int i = 0; i < EPC; ++i) o[q * EPC + i] = to_f32(e[i]);
   }
@@ -429,12 +460,32 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restric
           for (int v = 0; v < V; ++v) acc[u][s][v] = 0.f;
       }
     }
-    for (int e = 0; e < E4; e += EG) {
-      float dz[EG][U][V];
+    // PF: the next group's update loads are issued (raw) before this group is summed,
+    // so two groups of loads are in flight (E = 24: 4-slot 1078 -> 1028 us, 16-slot
+    // 2136 -> 1964 us at batch 256, D 1152)
+    constexpr bool PF = SIHC_WR_PF != 0;
+    RawVec<TW, V> dzr[PF ? EG : 1][PF ? U : 1];
+    auto issue = [&](int e) {
 #pragma unroll
       for (int q = 0; q < EG; ++q)
 #pragma unroll
-        for (int u = 0; u < U; ++u) load_vec<TW, V>(static_cast<const TW*>(upd.p[e + q]) + zoff[u], dz[q][u]);
+        for (int u = 0; u < U; ++u) load_raw<TW, V>(static_cast<const TW*>(upd.p[e + q]) + zoff[u], dzr[q][u]);
+    };
+    if constexpr (PF) issue(0);
+    for (int e = 0; e < E4; e += EG) {
+      float dz[EG][U][V];
+      if constexpr (PF) {
+#pragma unroll
+        for (int q = 0; q < EG; ++q)
+#pragma unroll
+          for (int u = 0; u < U; ++u) raw_to_f32<TW, V>(dzr[q][u], dz[q][u]);
+        if (e + EG < E4) issue(e + EG);
+      } else {
+#pragma unroll
+        for (int q = 0; q < EG; ++q)
+#pragma unroll
+          for (int u = 0; u < U; ++u) load_vec<TW, V>(static_cast<const TW*>(upd.p[e + q]) + zoff[u], dz[q][u]);
+      }
       load_fence();
       // Padded events (e + q >= E) loaded a repeated real update: zero the values
       // themselves (a zero weight times an Inf would still give NaN).
