@@ -90,9 +90,6 @@
 #define SIHC_WG_BCG 64
 #endif
 
-#ifndef SIHC_NT  // 1: non-temporal (streaming) hints on carrier/workspace traffic
-#define SIHC_NT 0
-#endif
 #ifndef SIHC_LOAD_FENCE  // 1: keep each token's loads ahead of its arithmetic (see load_fence)
 #define SIHC_LOAD_FENCE 1
 #endif
@@ -170,24 +167,29 @@ template <> struct RawT<8> { using type = u32x2; };
 template <> struct RawT<4> { using type = uint32_t; };
 template <> struct RawT<2> { using type = uint16_t; };
 
-template <typename R>
+// Stream access. NT = non-temporal hint: measured per kernel, it speeds up loads of
+// read-dominated streams (triangular with 3+ updates, gamma and weight gradients,
+// writes with 8+ events, reads with 1-2 events: 4-14%) and slows down balanced
+// read/write streams (per-event kernels, fused triangular backward: 1-3%) and slices
+// narrower than a 128-byte line (16-slot read/write with 16+ events: +40%).
+template <bool NT = false, typename R>
 __device__ __forceinline__ R ld(const R* p) {
-#if SIHC_NT
-  return __builtin_nontemporal_load(p);
-#else
-  return *p;
-#endif
+  if constexpr (NT) {
+    return __builtin_nontemporal_load(p);
+  } else {
+    return *p;
+  }
 }
-template <typename R>
+template <bool NT = false, typename R>
 __device__ __forceinline__ void st(R* p, R v) {
-#if SIHC_NT
-  __builtin_nontemporal_store(v, p);
-#else
-  *p = v;
-#endif
+  if constexpr (NT) {
+    __builtin_nontemporal_store(v, p);
+  } else {
+    *p = v;
+  }
 }
 
-template <typename T, int V>
+template <typename T, int V, bool NT = false>
 __device__ __forceinline__ void load_vec(const T* __restrict__ p, float* o) {
   constexpr int BYTES = V * int(sizeof(T));
   constexpr int CH = BYTES >= 16 ? 16 : BYTES;
@@ -195,7 +197,7 @@ __device__ __forceinline__ void load_vec(const T* __restrict__ p, float* o) {
   using R = typename RawT<CH>::type;
 #pragma unroll
   for (int q = 0; q < BYTES / CH; ++q) {
-    R r = ld(reinterpret_cast<const R*>(p) + q);
+    R r = ld<NT>(reinterpret_cast<const R*>(p) + q);
     T e[EPC];
     __builtin_memcpy(e, &r, CH);
 #pragma unroll
@@ -203,7 +205,7 @@ __device__ __forceinline__ void load_vec(const T* __restrict__ p, float* o) {
   }
 }
 
-template <typename T, int V>
+template <typename T, int V, bool NT = false>
 __device__ __forceinline__ void store_vec(T* __restrict__ p, const float* v) {
   constexpr int BYTES = V * int(sizeof(T));
   constexpr int CH = BYTES >= 16 ? 16 : BYTES;
@@ -216,7 +218,7 @@ __device__ __forceinline__ void store_vec(T* __restrict__ p, const float* v) {
     for (int i = 0; i < EPC; ++i) e[i] = from_f32<T>(v[q * EPC + i]);
     R r;
     __builtin_memcpy(&r, e, CH);
-    st(reinterpret_cast<R*>(p) + q, r);
+    st<NT>(reinterpret_cast<R*>(p) + q, r);
   }
 }
 
@@ -246,11 +248,11 @@ struct RawVec {
   using R = typename RawT<CH>::type;
   R r[BYTES / CH];
 };
-template <typename T, int V>
+template <typename T, int V, bool NT = false>
 __device__ __forceinline__ void load_raw(const T* __restrict__ p, RawVec<T, V>& o) {
   using RV = RawVec<T, V>;
 #pragma unroll
-  for (int q = 0; q < RV::BYTES / RV::CH; ++q) o.r[q] = ld(reinterpret_cast<const typename RV::R*>(p) + q);
+  for (int q = 0; q < RV::BYTES / RV::CH; ++q) o.r[q] = ld<NT>(reinterpret_cast<const typename RV::R*>(p) + q);
 }
 template <typename T, int V>
 __device__ __forceinline__ void raw_to_f32(const RawVec<T, V>& in, float* o) {
@@ -360,7 +362,7 @@ __device__ __forceinline__ void stage_weights(float* lds, const TW* __restrict__
 // read: out_e[m,c] = sum_s alpha[e,c,s] * x[m,s,c]
 // 1-D grid of (slices x chunks), block (BCG, TL); LDS holds alpha as [E][S][BC] fp32.
 // ----------------------------------------------------------------------------------
-template <typename T, int V, int K, int BCGT>
+template <typename T, int V, int K, int BCGT, bool NTL>
 __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict__ x, const T* __restrict__ alpha,
                                               PtrPack out, const int32_t* __restrict__ index,
                                               int E, Geo g, int tpb, int nslices) {
@@ -390,7 +392,7 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict_
       const int64_t p0 = cell_pixel0(mu, g, index);
       zoff[u] = int64_t(mu) * g.C + c0;
 #pragma unroll
-      for (int s = 0; s < S; ++s) load_vec<T, V>(x + slot_offset<K>(p0, s, g, c0), xv[u][s]);
+      for (int s = 0; s < S; ++s) load_vec<T, V, NTL>(x + slot_offset<K>(p0, s, g, c0), xv[u][s]);
     }
     load_fence();
     for (int e = 0; e < E; ++e) {
@@ -420,7 +422,7 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict_
 // Events are consumed in groups of 4 (E padded to a multiple of 4 with zero weights
 // and a repeated valid pointer), so each group's 4 update loads issue together.
 // ----------------------------------------------------------------------------------
-template <typename TX, typename TW, int V, int K, bool ADD_X, int BCGT>
+template <typename TX, typename TW, int V, int K, bool ADD_X, int BCGT, bool NTL>
 __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restrict__ x, PtrPack upd,
                                                const TW* __restrict__ beta, TX* __restrict__ out,
                                                const int32_t* __restrict__ index, int E, Geo g, int tpb,
@@ -452,7 +454,7 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restric
       zoff[u] = int64_t(mu) * g.C + c0;
       if constexpr (ADD_X) {
 #pragma unroll
-        for (int s = 0; s < S; ++s) load_vec<TX, V>(x + slot_offset<K>(p0[u], s, g, c0), acc[u][s]);
+        for (int s = 0; s < S; ++s) load_vec<TX, V, NTL>(x + slot_offset<K>(p0[u], s, g, c0), acc[u][s]);
       } else {
 #pragma unroll
         for (int s = 0; s < S; ++s)
@@ -469,7 +471,7 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restric
 #pragma unroll
       for (int q = 0; q < EG; ++q)
 #pragma unroll
-        for (int u = 0; u < U; ++u) load_raw<TW, V>(static_cast<const TW*>(upd.p[e + q]) + zoff[u], dzr[q][u]);
+        for (int u = 0; u < U; ++u) load_raw<TW, V, NTL>(static_cast<const TW*>(upd.p[e + q]) + zoff[u], dzr[q][u]);
     };
     if constexpr (PF) issue(0);
     for (int e = 0; e < E4; e += EG) {
@@ -484,7 +486,7 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restric
 #pragma unroll
         for (int q = 0; q < EG; ++q)
 #pragma unroll
-          for (int u = 0; u < U; ++u) load_vec<TW, V>(static_cast<const TW*>(upd.p[e + q]) + zoff[u], dz[q][u]);
+          for (int u = 0; u < U; ++u) load_vec<TW, V, NTL>(static_cast<const TW*>(upd.p[e + q]) + zoff[u], dz[q][u]);
       }
       load_fence();
       // Padded events (e + q >= E) loaded a repeated real update: zero the values
@@ -554,6 +556,7 @@ __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack 
                                                const int32_t* __restrict__ index, int E, Geo g, int tpb,
                                                int nslices, int TT, PtrPack dout, const void* __restrict__ gam,
                                                int gam_f32) {
+  constexpr bool NTL = !STORE_D;  // non-temporal loads, except in the fused triangular backward
   constexpr int S = CARRIER ? K * K : 1;
   static_assert(!(STORE_D && CARRIER), "update gradients exist only in workspace mode");
   extern __shared__ float xt[];  // [TT*S rows][BCG*V], lds_w layout
@@ -608,7 +611,7 @@ __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack 
           } else {
             off = int64_t(m) * g.C + ci;
           }
-          load_vec<T, V>(x + off, v8[q]);
+          load_vec<T, V, NTL>(x + off, v8[q]);
         } else {
 #pragma unroll
           for (int v = 0; v < V; ++v) v8[q][v] = 0.f;
@@ -633,7 +636,7 @@ __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack 
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
           const int tq = min(t + q, tn - 1);  // clamp: a repeated token is loaded, not added
-          load_vec<T, V>(ze + int64_t(t0 + tq) * g.C + c0, zv[q]);
+          load_vec<T, V, NTL>(ze + int64_t(t0 + tq) * g.C + c0, zv[q]);
         }
         load_fence();
 #pragma unroll
@@ -677,6 +680,7 @@ __global__ void __launch_bounds__(256) k_wgrad_direct(const T* __restrict__ x, P
                                                       const int32_t* __restrict__ index, int E, Geo g, int tpb,
                                                       int nslices, PtrPack dout, const void* __restrict__ gam,
                                                       int gam_f32) {
+  constexpr bool NTL = true;
   constexpr int S = CARRIER ? K * K : 1;
   constexpr int TG = CARRIER ? 2 : 4;
   static_assert(!(STORE_D && CARRIER), "update gradients exist only in workspace mode");
@@ -711,11 +715,11 @@ __global__ void __launch_bounds__(256) k_wgrad_direct(const T* __restrict__ x, P
       if constexpr (CARRIER) {
         const int64_t p0 = cell_pixel0(mq, g, index);
 #pragma unroll
-        for (int s = 0; s < S; ++s) load_vec<T, V>(x + slot_offset<K>(p0, s, g, c0), xv[q][s]);
+        for (int s = 0; s < S; ++s) load_vec<T, V, NTL>(x + slot_offset<K>(p0, s, g, c0), xv[q][s]);
       } else {
-        load_vec<T, V>(x + int64_t(mq) * g.C + c0, xv[q][0]);
+        load_vec<T, V, NTL>(x + int64_t(mq) * g.C + c0, xv[q][0]);
       }
-      load_vec<T, V>(ze + int64_t(mq) * g.C + c0, zv[q]);
+      load_vec<T, V, NTL>(ze + int64_t(mq) * g.C + c0, zv[q]);
     }
     load_fence();
 #pragma unroll
@@ -897,6 +901,7 @@ __global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgradz(const bf16_t* __
                                                                 float* __restrict__ part,
                                                                 const int32_t* __restrict__ index, int E, Geo g,
                                                                 int tpb, int nslices) {
+  constexpr bool NTL = true;
   constexpr int S = K * K, TT = SIHC_C16Z_TT, VS = 8, NV = C16_LANES / VS;
   constexpr int NXV = TT * S * NV;  // carrier vectors per tile
   constexpr int NZQ = EPL;  // update rows (events) staged per wave: ceil(E / ceil(E / EPL)) <= EPL
@@ -928,11 +933,11 @@ __global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgradz(const bf16_t* __
     }
     const int64_t zoff = int64_t(t0 + min(zt_t, tn - 1)) * g.C + (zc < g.C ? zc : cs);
 #pragma unroll
-    for (int k = 0; k < NXQ; ++k) xb[k] = ld(reinterpret_cast<const R*>(x + off[k]));
+    for (int k = 0; k < NXQ; ++k) xb[k] = ld<NTL>(reinterpret_cast<const R*>(x + off[k]));
 #pragma unroll
     for (int k = 0; k < NZQ; ++k) {
       const int e = min(wave + k * nw, E - 1);
-      zb[k] = ld(reinterpret_cast<const R*>(static_cast<const bf16_t*>(z.p[e]) + zoff));
+      zb[k] = ld<NTL>(reinterpret_cast<const R*>(static_cast<const bf16_t*>(z.p[e]) + zoff));
     }
   };
   auto commit = [&](int tn) {
@@ -1047,7 +1052,7 @@ __global__ void __launch_bounds__(256) k_fill_zero(TO* __restrict__ out, int64_t
 // triangular: out[m,c] = base[m,c] + sum_j gamma[j,c] * upd_j[m,c]
 // (active count padded to a multiple of 4 with zero gamma rows, as in k_write)
 // ----------------------------------------------------------------------------------
-template <typename T, typename TG, int V>
+template <typename T, typename TG, int V, bool NTL>
 __global__ void __launch_bounds__(256) k_triangular(const T* __restrict__ base, PtrPack upd,
                                                     const TG* __restrict__ gamma, T* __restrict__ out,
                                                     int A, int M, int C, int tpb, int nslices) {
@@ -1079,14 +1084,14 @@ __global__ void __launch_bounds__(256) k_triangular(const T* __restrict__ base, 
     for (int u = 0; u < U; ++u) {
       ok[u] = m + u * TL < m_end;
       off[u] = int64_t(ok[u] ? m + u * TL : m) * C + c0;
-      load_vec<T, V>(base + off[u], acc[u]);
+      load_vec<T, V, NTL>(base + off[u], acc[u]);
     }
     for (int j = 0; j < A4; j += 4) {
       float dz[4][U][V];
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int u = 0; u < U; ++u) load_vec<T, V>(static_cast<const T*>(upd.p[j + q]) + off[u], dz[q][u]);
+        for (int u = 0; u < U; ++u) load_vec<T, V, NTL>(static_cast<const T*>(upd.p[j + q]) + off[u], dz[q][u]);
       load_fence();
 #pragma unroll
       for (int q = 0; q < 4; ++q)
@@ -1810,12 +1815,18 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
           if constexpr (KK == 4 && VV > SIHC_RW_VEC_K4) {
             return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
           } else {
+            // non-temporal carrier loads: for 1-2 events (4 slots) or up to 12 (16 slots),
+            // and only with slice rows of whole 128-byte lines
+            const bool ntl = sh.bcg * VV * int(sizeof(T)) >= 128 && events <= (KK == 2 ? 2 : 12);
             return with_bcg<KK>(sh.bcg, [&](auto bb) {
               constexpr int BB = decltype(bb)::value;
-              hipLaunchKernelGGL((k_read<T, VV, KK, BB>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), lds,
-                                 st, static_cast<const T*>(x), static_cast<const T*>(alpha), pk, index, events, g,
-                                 tpb, sh.slices);
-              return check_launch(what);
+              return with_bool(ntl, [&](auto nt) {
+                constexpr bool NT = decltype(nt)::value;
+                hipLaunchKernelGGL((k_read<T, VV, KK, BB, NT>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl),
+                                   lds, st, static_cast<const T*>(x), static_cast<const T*>(alpha), pk, index, events,
+                                   g, tpb, sh.slices);
+                return check_launch(what);
+              });
             });
           }
         });
@@ -1865,15 +1876,20 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
           if constexpr (KK == 4 && VV > SIHC_RW_VEC_K4) {
             return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
           } else {
+            // non-temporal loads with 8+ events and slice rows of whole 128-byte lines
+            const bool ntl = sh.bcg * VV * int(sizeof(TX)) >= 128 && events >= 8;
             return with_bool(add_x != 0, [&](auto ax) {
               constexpr bool AX = decltype(ax)::value;
               return with_bcg<KK>(sh.bcg, [&](auto bb) {
                 constexpr int BB = decltype(bb)::value;
-                hipLaunchKernelGGL((k_write<TX, TW, VV, KK, AX, BB>), dim3(blocks1d(sh.slices, chunks)),
-                                   dim3(sh.bcg, sh.tl), lds, st, static_cast<const TX*>(x), pk,
-                                   static_cast<const TW*>(beta), static_cast<TX*>(out), index, events, g, tpb,
-                                   sh.slices);
-                return check_launch(what);
+                return with_bool(ntl, [&](auto nt) {
+                  constexpr bool NT = decltype(nt)::value;
+                  hipLaunchKernelGGL((k_write<TX, TW, VV, KK, AX, BB, NT>), dim3(blocks1d(sh.slices, chunks)),
+                                     dim3(sh.bcg, sh.tl), lds, st, static_cast<const TX*>(x), pk,
+                                     static_cast<const TW*>(beta), static_cast<TX*>(out), index, events, g, tpb,
+                                     sh.slices);
+                  return check_launch(what);
+                });
               });
             });
           }
@@ -1941,10 +1957,14 @@ int sihc_triangular(const void* base, const void* const* updates, const void* ga
         if constexpr (VV * sizeof(T) > 16) {
           return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
         } else {
-          hipLaunchKernelGGL((k_triangular<T, TG, VV>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), lds,
-                             st, static_cast<const T*>(base), pk, static_cast<const TG*>(gamma), static_cast<T*>(out),
-                             active, int(rows), channels, tpb, sh.slices);
-          return check_launch(what);
+          // non-temporal loads with 3+ updates (read-dominated: (A + 1) rows in, 1 out)
+          return with_bool(active >= 3, [&](auto nt) {
+            constexpr bool NT = decltype(nt)::value;
+            hipLaunchKernelGGL((k_triangular<T, TG, VV, NT>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl),
+                               lds, st, static_cast<const T*>(base), pk, static_cast<const TG*>(gamma),
+                               static_cast<T*>(out), active, int(rows), channels, tpb, sh.slices);
+            return check_launch(what);
+          });
         }
       });
     });
