@@ -134,3 +134,27 @@ def test_hip_graph_capture_of_event_backward_chain():
         ex, ed = run(nx.clone().requires_grad_(), nd.clone().requires_grad_())
         torch.cuda.synchronize()
         assert torch.equal(gx, ex) and torch.equal(gd, ed), f"replay {r} differs from eager"
+
+
+def test_hip_graph_capture_of_a_cold_weight_gradient():
+    # The pipelined weight-gradient kernel sizes its grid from an occupancy query (host
+    # side, cached per kernel shape) on the first launch of a shape. Here that first
+    # launch happens inside the capture: the replays must match eager calls bit for bit.
+    announce("hip graph weight gradient, first launch of its shape inside the capture")
+    torch.manual_seed(5)
+    from sihc_hip import launch
+
+    x = torch.randn(2, 32, 32, 72, device="cuda").to(torch.bfloat16)  # 4-slot cells, 13 events
+    ups = [torch.randn(2, 256, 72, device="cuda").to(torch.bfloat16) for _ in range(13)]
+    w = torch.randn(13, 72, 4, device="cuda").to(torch.bfloat16)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static_out = launch.weight_grad(x, ups, w, out_dtype=torch.float32)
+    for r in range(3):
+        with torch.no_grad():
+            x.copy_(torch.randn_like(x.float()).to(torch.bfloat16))
+        graph.replay()
+        expected = launch.weight_grad(x, ups, w, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, expected), f"replay {r} differs from eager"
