@@ -3,8 +3,9 @@
 The kernels treat tokens independently, so per-token outputs are checked on batch
 slices against the CPU oracle; token reductions (weight gradients) are checked
 against float64 CPU sums on channel slices; everything is checked for bitwise
-run-to-run determinism. One case uses a carrier with more than 2**31 elements to
-exercise 64-bit addressing.
+run-to-run determinism. Two cases use a carrier with more than 2**31 elements to
+exercise 64-bit addressing (the per-event forward, and the stage read / write / weight
+gradient).
 """
 from __future__ import annotations
 
@@ -109,4 +110,37 @@ def test_carrier_over_2_pow_31_elements():
     assert_parity(x_out[sl], rx, BF16, what="x_out tail")
     assert_parity(z_out[sl], rz, BF16, what="z_out tail")
     del x, x_out, z_out, dz
+    torch.cuda.empty_cache()
+
+
+def test_stage_ops_over_2_pow_31_carrier_elements():
+    # The stage kernels at the same 2.42e9-element carrier (64-bit offsets in every
+    # kernel shape: non-temporal reads with 2 events, 8-event reads and writes, the
+    # pipelined weight gradient). Per-token outputs are checked on the last two batch
+    # items; the weight gradient gets updates that are zero outside those items, so its
+    # full-size reduction equals the oracle's sum over that slice.
+    announce("max size carrier B2048 D1152 bf16 stage ops")
+    B, C, E = 2048, 1152, 8
+    g = torch.Generator(device="cuda").manual_seed(6)
+    x = torch.randn(B, 32, 32, C, device="cuda", generator=g).to(BF16)
+    assert x.numel() > 2 ** 31
+    w = (0.2 + 0.05 * torch.randn(E, C, 4, device="cuda", generator=g)).to(BF16)
+    sl = slice(B - 2, B)
+    xs = x[sl].cpu()
+    for e in (2, E):
+        got = launch.read(x, w[:e].contiguous())
+        exp = O.read(xs, w[:e].cpu())
+        for i in range(e):
+            assert_parity(got[i][sl], exp[i], BF16, what=f"read E={e} output {i} tail")
+        del got
+    ups = [torch.zeros(B, 256, C, device="cuda", dtype=BF16) for _ in range(E)]
+    for u in ups:
+        u[sl] = torch.randn(2, 256, C, device="cuda", generator=g).to(BF16)
+    out = launch.write(x, ups, w)
+    assert_parity(out[sl], O.write(xs, [u[sl].cpu() for u in ups], w.cpu()), BF16, what="write tail")
+    del out
+    torch.cuda.empty_cache()
+    wg = launch.weight_grad(x, ups, w, out_dtype=torch.float32)
+    assert_parity(wg, O.weight_grad(xs, [u[sl].cpu() for u in ups], 4), torch.float32, what="weight grad")
+    del x, ups, wg
     torch.cuda.empty_cache()
