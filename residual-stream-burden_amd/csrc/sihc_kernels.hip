@@ -5,17 +5,20 @@
 // There is no matrix-core work: per element the path does at most 2*E*S flops per
 // 2*(S+E) bytes.
 //
-// Thread mapping shared by every kernel: a block is (BCG channel groups) x (TL token
-// lanes). A lane owns V adjacent channels (up to one 16-byte vector) and walks a run of
-// tokens with stride TL, so each wave issues fully coalesced vector loads, and the
-// per-channel weights of its channel group are fetched once per block: into LDS when
-// the kernel handles many events (read / write / triangular), into registers when it
-// handles one (per-event fused kernels). Every token is processed as "issue all loads,
-// then compute, then store" with no data-dependent branches in the loop body, so each
-// lane keeps all of a token's loads in flight at once. All sums are fp32 with a single
-// round-to-nearest-even per stored element. Reductions over tokens (weight gradients)
-// are per-lane fp32 partials, then one LDS pass per block that writes a per-block
-// partial row, then a fixed-order sum over blocks: no atomics, bitwise deterministic.
+// Thread mapping of most kernels: a block is (BCG channel groups) x (TL token lanes).
+// A lane owns V adjacent channels (up to one 16-byte vector) and walks a run of tokens
+// with stride TL, so each wave issues fully coalesced vector loads, and the per-channel
+// weights of its channel group are fetched once per block: into LDS when the kernel
+// handles many events (read / write / triangular), into registers when it handles one
+// (per-event fused kernels). Every token is processed as "issue all loads, then
+// compute, then store" with no data-dependent branches in the loop body, so each lane
+// keeps all of a token's loads in flight at once (the write also issues the next event
+// group's loads early). The pipelined carrier weight gradient instead gives each lane
+// one channel and stages whole tiles of rows in LDS with 16-byte loads, one tile ahead.
+// All sums are fp32 with a single round-to-nearest-even per stored element. Reductions
+// over tokens (weight gradients) are per-lane fp32 partials (for the per-event backward,
+// one LDS pass per block), a per-block partial row, then a fixed-order sum over blocks:
+// no atomics, bitwise deterministic.
 //
 // Reference (behaviour, not code): tongtongliang/residual-stream-burden,
 // sihc/models/sihc/sublayer_kernels.py (Triton `_read`, `_write`, `_weight_grad`,
