@@ -59,6 +59,12 @@
 #ifndef SIHC_EV_CHUNK  // tokens per reduction chunk, per-event backward
 #define SIHC_EV_CHUNK 256
 #endif
+#ifndef SIHC_EV_GROUP  // tokens per interleaved group of a backward chunk (0: contiguous)
+#define SIHC_EV_GROUP 64
+#endif
+#ifndef SIHC_EV_BWD_NT  // non-temporal hints in the per-event backward: 1 loads, 2 stores, 3 both
+#define SIHC_EV_BWD_NT 0
+#endif
 #ifndef SIHC_RW_BCG  // channel-group lanes per block, read / write / triangular
 #define SIHC_RW_BCG 16
 #endif
@@ -1193,13 +1199,14 @@ __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_fwd(const T* __rest
 //   HAS_W: write part (dz, beta)  STORE_T: store t as grad_x (else the caller aliases)
 // part[chunk][0][s][c] = partial grad_beta, part[chunk][1][s][c] = partial grad_alpha_next
 // ----------------------------------------------------------------------------------
-template <typename T, int V, int K, bool HAS_H, bool HAS_G, bool HAS_W, bool STORE_T>
+template <typename T, int V, int K, bool HAS_H, bool HAS_G, bool HAS_W, bool STORE_T, bool NTL, bool NTS>
 __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_bwd(const T* __restrict__ gxo, const T* __restrict__ gzo,
                                                    const T* __restrict__ xo, const T* __restrict__ dz,
                                                    const T* __restrict__ beta,
                                                    const T* __restrict__ alpha, T* __restrict__ gx,
                                                    T* __restrict__ gdz, float* __restrict__ part,
-                                                   const int32_t* __restrict__ index, Geo g, int tpb, int nslices) {
+                                                   const int32_t* __restrict__ index, Geo g, int gs, int nchunks,
+                                                   int nslices) {
   constexpr int S = K * K;
   constexpr int U = SIHC_EV_UNROLL;  // tokens per lane per iteration
   extern __shared__ float red[];
@@ -1219,77 +1226,84 @@ __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_bwd(const T* __rest
     float bw[S][V], aw[S][V];
     if constexpr (HAS_W) load_weights<T, V, K>(beta, c0, bw);
     if constexpr (HAS_G) load_weights<T, V, K>(alpha, c0, aw);
-    const int m_begin = chunk * tpb;
-    const int m_end = min(m_begin + tpb, g.M);
-    for (int m = m_begin + threadIdx.y; m < m_end; m += U * TL) {
-      int64_t p0[U], zoff[U];
-      bool ok[U];
-      float gz[U][V], d[U][V], t[U][S][V], xv[U][S][V];
-      // ---- loads (tail tokens reload a valid token; their values are zeroed below so
-      //      they add nothing to the weight gradients, and nothing is stored)
+    // The chunk's tokens: groups of gs tokens (a multiple of U * TL), group `chunk`
+    // and every nchunks-th one after it, so the blocks resident at one time work on
+    // neighbouring groups and the device streams through a narrow window of each array.
+    const int64_t M = g.M;
+    // one token's compute and stores (tail tokens: zero every loaded value so it adds
+    // exactly nothing -- a zero factor alone would turn an Inf in the repeated token
+    // into NaN -- and store nothing)
+    auto consume = [&](float (&gz)[V], float (&d)[V], float (&t)[S][V], float (&xv)[S][V], int64_t p0,
+                       int64_t zoff, bool ok) {
+      if (!ok) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        ok[u] = m + u * TL < m_end;
-        const int mu = ok[u] ? m + u * TL : m;
-        p0[u] = cell_pixel0(mu, g, index);
-        zoff[u] = int64_t(mu) * g.C + c0;
-        if constexpr (HAS_G) load_vec<T, V>(gzo + zoff[u], gz[u]);
-        if constexpr (HAS_W) load_vec<T, V>(dz + zoff[u], d[u]);
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-          const int64_t off = slot_offset<K>(p0[u], s, g, c0);
-          if constexpr (HAS_H) {
-            load_vec<T, V>(gxo + off, t[u][s]);
-          } else {
-#pragma unroll
-            for (int v = 0; v < V; ++v) t[u][s][v] = 0.f;
-          }
-          if constexpr (HAS_G) load_vec<T, V>(xo + off, xv[u][s]);
+        for (int v = 0; v < V; ++v) {
+          gz[v] = 0.f;
+          d[v] = 0.f;
         }
+#pragma unroll
+        for (int ss = 0; ss < S; ++ss)
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            t[ss][v] = 0.f;
+            xv[ss][v] = 0.f;
+          }
       }
-      load_fence();
-      // ---- compute and store
+      float gd[V];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        if (U > 1 && !ok[u]) {
-          // tail token: zero every loaded value so it adds exactly nothing (a zero
-          // factor alone would turn an Inf in the repeated token into NaN)
+      for (int v = 0; v < V; ++v) gd[v] = 0.f;
 #pragma unroll
-          for (int v = 0; v < V; ++v) {
-            gz[u][v] = 0.f;
-            d[u][v] = 0.f;
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          if constexpr (HAS_G) {
+            da[s][v] = fmaf(xv[s][v], gz[v], da[s][v]);
+            t[s][v] = fmaf(aw[s][v], gz[v], t[s][v]);
           }
-#pragma unroll
-          for (int ss = 0; ss < S; ++ss)
-#pragma unroll
-            for (int v = 0; v < V; ++v) {
-              t[u][ss][v] = 0.f;
-              xv[u][ss][v] = 0.f;
-            }
+          if constexpr (HAS_W) {
+            gd[v] = fmaf(bw[s][v], t[s][v], gd[v]);
+            db[s][v] = fmaf(d[v], t[s][v], db[s][v]);
+          }
         }
-        float gd[V];
+      if (ok) {
+        if constexpr (STORE_T) {
 #pragma unroll
-        for (int v = 0; v < V; ++v) gd[v] = 0.f;
-#pragma unroll
-        for (int s = 0; s < S; ++s)
-#pragma unroll
-          for (int v = 0; v < V; ++v) {
-            if constexpr (HAS_G) {
-              da[s][v] = fmaf(xv[u][s][v], gz[u][v], da[s][v]);
-              t[u][s][v] = fmaf(aw[s][v], gz[u][v], t[u][s][v]);
-            }
-            if constexpr (HAS_W) {
-              gd[v] = fmaf(bw[s][v], t[u][s][v], gd[v]);
-              db[s][v] = fmaf(d[u][v], t[u][s][v], db[s][v]);
-            }
-          }
-        if (ok[u]) {
-          if constexpr (STORE_T) {
-#pragma unroll
-            for (int s = 0; s < S; ++s) store_vec<T, V>(gx + slot_offset<K>(p0[u], s, g, c0), t[u][s]);
-          }
-          if constexpr (HAS_W) store_vec<T, V>(gdz + zoff[u], gd);
+          for (int s = 0; s < S; ++s) store_vec<T, V, NTS>(gx + slot_offset<K>(p0, s, g, c0), t[s]);
         }
+        if constexpr (HAS_W) store_vec<T, V, NTS>(gdz + zoff, gd);
+      }
+    };
+    for (int64_t m0 = int64_t(chunk) * gs; m0 < M; m0 += int64_t(nchunks) * gs) {
+      const int64_t m_end = min(m0 + gs, M);
+      for (int64_t mi = m0; mi < m_end; mi += U * TL) {
+        int64_t p0[U], zoff[U];
+        bool ok[U];
+        float gz[U][V], d[U][V], t[U][S][V], xv[U][S][V];
+        // loads (tail tokens reload the iteration's first token, which is valid)
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int64_t mt = mi + threadIdx.y + u * TL;
+          ok[u] = mt < m_end;
+          const int mu = int(ok[u] ? mt : mi);
+          p0[u] = cell_pixel0(mu, g, index);
+          zoff[u] = int64_t(mu) * g.C + c0;
+          if constexpr (HAS_G) load_vec<T, V, NTL>(gzo + zoff[u], gz[u]);
+          if constexpr (HAS_W) load_vec<T, V, NTL>(dz + zoff[u], d[u]);
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            const int64_t off = slot_offset<K>(p0[u], s, g, c0);
+            if constexpr (HAS_H) {
+              load_vec<T, V, NTL>(gxo + off, t[u][s]);
+            } else {
+#pragma unroll
+              for (int v = 0; v < V; ++v) t[u][s][v] = 0.f;
+            }
+            if constexpr (HAS_G) load_vec<T, V, NTL>(xo + off, xv[u][s]);
+          }
+        }
+        load_fence();
+#pragma unroll
+        for (int u = 0; u < U; ++u) consume(gz[u], d[u], t[u], xv[u], p0[u], zoff[u], ok[u]);
       }
     }
   }
@@ -1449,6 +1463,14 @@ int wgrad_chunks(int64_t M, int events, int C) {
   return int(std::max<int64_t>(base, std::min(want, cap)));
 }
 int event_bwd_chunks(int64_t M) { return chunk_count(M, SIHC_EV_CHUNK, 512); }
+
+// Tokens per interleaved group of a reduction chunk (chunk c takes groups c, c + chunks,
+// ...): `want` rounded up to a multiple of `step` (the tokens of one loop iteration or
+// tile); want = 0 gives each chunk one contiguous run.
+int group_tokens(int want, int64_t M, int chunks, int step) {
+  const int64_t w = want > 0 ? want : (M + chunks - 1) / std::max(chunks, 1);
+  return int((std::max<int64_t>(w, 1) + step - 1) / step * step);
+}
 
 // Compute units of the current device (cached per device; 0 if unknown).
 int device_cus() {
@@ -2143,15 +2165,18 @@ int sihc_event_backward(const void* grad_x_out, const void* grad_z_out, const vo
             constexpr bool HH = decltype(hh)::value;
             auto go = [&](auto hg, auto hw, auto stt) {
               constexpr bool HG = decltype(hg)::value, HW = decltype(hw)::value, STT = decltype(stt)::value;
-              const void* kfn = reinterpret_cast<const void*>(&k_event_bwd<T, VV, KK, HH, HG, HW, STT>);
+              constexpr bool NTL = (SIHC_EV_BWD_NT & 1) != 0, NTS = (SIHC_EV_BWD_NT & 2) != 0;
+              const void* kfn = reinterpret_cast<const void*>(&k_event_bwd<T, VV, KK, HH, HG, HW, STT, NTL, NTS>);
               chunks = whole_rounds(sh.slices, max_chunks, resident_blocks(kfn, sh.bcg * sh.tl, lds));
-              const int tpb = int((int64_t(g.M) + chunks - 1) / chunks);
-              hipLaunchKernelGGL((k_event_bwd<T, VV, KK, HH, HG, HW, STT>), dim3(blocks1d(sh.slices, chunks)),
+              // token groups: a multiple of one loop iteration (SIHC_EV_UNROLL x TL tokens);
+              // group 0 means one contiguous run of tokens per chunk
+              const int gs = group_tokens(SIHC_EV_GROUP, g.M, chunks, SIHC_EV_UNROLL * sh.tl);
+              hipLaunchKernelGGL((k_event_bwd<T, VV, KK, HH, HG, HW, STT, NTL, NTS>), dim3(blocks1d(sh.slices, chunks)),
                                  dim3(sh.bcg, sh.tl), lds, st, static_cast<const T*>(grad_x_out),
                                  static_cast<const T*>(grad_z_out), static_cast<const T*>(x_out),
                                  static_cast<const T*>(dz), static_cast<const T*>(beta),
                                  static_cast<const T*>(alpha_next), static_cast<T*>(grad_x), static_cast<T*>(grad_dz),
-                                 part, index, g, tpb, sh.slices);
+                                 part, index, g, gs, chunks, sh.slices);
               return check_launch(what);
             };
             switch (mode) {

@@ -65,6 +65,35 @@ def test_event_backward_matches_adjoint(dtype, slots, has_h, has_g):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("slots,batch,grid", [(4, 37, 15), (16, 9, 13)])
+def test_event_backward_many_interleaved_chunks(dtype, slots, batch, grid):
+    # Tens of reduction chunks, each taking every chunks-th group of 64 tokens; the token
+    # count (8325 and 1521) leaves a short last group and the 136 channels a short last
+    # channel slice, with a per-batch state permutation.
+    announce(f"event bwd chunks dtype={dtype} slots={slots} b={batch} g={grid}")
+    torch.manual_seed(31)
+    k = O.cell_edge(slots)
+    c = 136
+    x_out = torch.randn(batch, grid * k, grid * k, c, device="cuda", dtype=dtype)
+    dz = torch.randn(batch, grid * grid, c, device="cuda", dtype=dtype)
+    beta = (1.0 + 0.02 * torch.randn(c, slots, device="cuda")).to(dtype)
+    alpha = (1.0 / slots + 0.02 * torch.randn(c, slots, device="cuda")).to(dtype)
+    h = 1e-2 * torch.randn_like(x_out)
+    g = 1e-2 * torch.randn_like(dz)
+    gen = torch.Generator().manual_seed(5)
+    index = torch.stack([torch.randperm(grid * grid, generator=gen) for _ in range(batch)]).to(torch.int32)
+    got = launch.event_backward(h, g, x_out, dz, beta, alpha, index=index.cuda())
+    cells = lambda t: O.cells_to_high(O.gather_cells(t.cpu(), index, slots))
+    ref = O.event_backward(cells(h), g.cpu(), cells(x_out), dz.cpu(), beta.cpu(), alpha.cpu())
+    assert_parity(O.cells_to_high(O.gather_cells(got[0].cpu(), index, slots)), ref[0], dtype, what="grad_x")
+    for name, a, b in zip(("grad_dz", "grad_beta", "grad_alpha_next"), got[1:], ref[1:]):
+        assert_parity(a, b, dtype, what=name)
+    again = launch.event_backward(h, g, x_out, dz, beta, alpha, index=index.cuda())
+    for a, b in zip(got, again):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("slots", [4, 16])
 def test_literal_stage_forward_and_gradients(dtype, slots):
     # Literal per-event schedule on HIP vs the oracle's literal schedule
