@@ -63,7 +63,10 @@
 #define SIHC_EV_GROUP 64
 #endif
 #ifndef SIHC_EV_BWD_NT  // non-temporal hints in the per-event backward: 1 loads, 2 stores, 3 both
-#define SIHC_EV_BWD_NT 0
+#define SIHC_EV_BWD_NT 3
+#endif
+#ifndef SIHC_EV_FWD_NT  // non-temporal hints in the per-event forward: 1 loads, 2 stores, 3 both
+#define SIHC_EV_FWD_NT 3
 #endif
 #ifndef SIHC_RW_BCG  // channel-group lanes per block, read / write / triangular
 #define SIHC_RW_BCG 16
@@ -192,6 +195,10 @@ __device__ __forceinline__ R ld(const R* p) {
 template <bool NT = false, typename R>
 __device__ __forceinline__ void st(R* p, R v) {
   if constexpr (NT) {
+    // An empty register constraint keeps the stored words opaque: otherwise the
+    // optimizer folds the bf16 conversion into the store, retypes it as a bfloat
+    // vector store and drops the non-temporal hint (checked in the generated code).
+    asm volatile("" : "+v"(v));
     __builtin_nontemporal_store(v, p);
   } else {
     *p = v;
@@ -1139,7 +1146,7 @@ __device__ __forceinline__ void load_weights(const T* __restrict__ w, int c0, fl
     for (int s = 0; s < S; ++s) out[s][v] = tmp[v * S + s];
 }
 
-template <typename T, int V, int K, bool HAS_Z>
+template <typename T, int V, int K, bool HAS_Z, bool NTL, bool NTS>
 __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_fwd(const T* __restrict__ x, const T* __restrict__ dz,
                                                    const T* __restrict__ beta,
                                                    const T* __restrict__ alpha, T* __restrict__ xo,
@@ -1167,9 +1174,9 @@ __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_fwd(const T* __rest
       const int mu = ok[u] ? m + u * TL : m;  // tail: reload a valid token, store nothing
       p0[u] = cell_pixel0(mu, g, index);
       zoff[u] = int64_t(mu) * g.C + c0;
-      load_vec<T, V>(dz + zoff[u], d[u]);
+      load_vec<T, V, NTL>(dz + zoff[u], d[u]);
 #pragma unroll
-      for (int s = 0; s < S; ++s) load_vec<T, V>(x + slot_offset<K>(p0[u], s, g, c0), xv[u][s]);
+      for (int s = 0; s < S; ++s) load_vec<T, V, NTL>(x + slot_offset<K>(p0[u], s, g, c0), xv[u][s]);
     }
     load_fence();
 #pragma unroll
@@ -1186,8 +1193,8 @@ __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_fwd(const T* __rest
         }
       if (ok[u]) {
 #pragma unroll
-        for (int s = 0; s < S; ++s) store_vec<T, V>(xo + slot_offset<K>(p0[u], s, g, c0), xv[u][s]);
-        if constexpr (HAS_Z) store_vec<T, V>(zo + zoff[u], zacc);
+        for (int s = 0; s < S; ++s) store_vec<T, V, NTS>(xo + slot_offset<K>(p0[u], s, g, c0), xv[u][s]);
+        if constexpr (HAS_Z) store_vec<T, V, NTS>(zo + zoff[u], zacc);
       }
     }
   }
@@ -2086,7 +2093,8 @@ int sihc_event_forward(const void* x, const void* dz, const void* beta, const vo
         } else {
           return with_bool(alpha_next != nullptr, [&](auto hz) {
             constexpr bool HZ = decltype(hz)::value;
-            hipLaunchKernelGGL((k_event_fwd<T, VV, KK, HZ>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), 0,
+            constexpr bool NTL = (SIHC_EV_FWD_NT & 1) != 0, NTS = (SIHC_EV_FWD_NT & 2) != 0;
+            hipLaunchKernelGGL((k_event_fwd<T, VV, KK, HZ, NTL, NTS>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), 0,
                                st, static_cast<const T*>(x), static_cast<const T*>(dz), static_cast<const T*>(beta),
                                static_cast<const T*>(alpha_next), static_cast<T*>(x_out), static_cast<T*>(z_out),
                                index, g, tpb, sh.slices);
