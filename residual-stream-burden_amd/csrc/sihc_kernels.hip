@@ -68,6 +68,26 @@
 #ifndef SIHC_EV_FWD_NT  // non-temporal hints in the per-event forward: 1 loads, 2 stores, 3 both
 #define SIHC_EV_FWD_NT 3
 #endif
+// Non-temporal hint modes (1 loads, 2 stores, 3 both) of the stage kernels; -1 selects
+// by launch shape.
+#ifndef SIHC_RD_NTM
+#define SIHC_RD_NTM -1
+#endif
+#ifndef SIHC_WR_NTM
+#define SIHC_WR_NTM -1
+#endif
+#ifndef SIHC_TRI_NTM
+#define SIHC_TRI_NTM -1
+#endif
+#ifndef SIHC_TRIB_NTM  // the fused triangular backward (weight-gradient kernels storing d)
+#define SIHC_TRIB_NTM -1
+#endif
+#ifndef SIHC_CELLS_NTM  // gather / scatter of cells (both hinted: 7% faster)
+#define SIHC_CELLS_NTM 3
+#endif
+#ifndef SIHC_COPY_NTM  // the library's copy (both hinted: 16% faster)
+#define SIHC_COPY_NTM 3
+#endif
 #ifndef SIHC_RW_BCG  // channel-group lanes per block, read / write / triangular
 #define SIHC_RW_BCG 16
 #endif
@@ -179,11 +199,13 @@ template <> struct RawT<8> { using type = u32x2; };
 template <> struct RawT<4> { using type = uint32_t; };
 template <> struct RawT<2> { using type = uint16_t; };
 
-// Stream access. NT = non-temporal hint: measured per kernel, it speeds up loads of
-// read-dominated streams (triangular with 3+ updates, gamma and weight gradients,
-// writes with 8+ events, reads with 1-2 events: 4-14%) and slows down balanced
-// read/write streams (per-event kernels, fused triangular backward: 1-3%) and slices
-// narrower than a 128-byte line (16-slot read/write with 16+ events: +40%).
+// Stream access. NT = non-temporal hint (the `nt` bit of the global load / store). Chosen
+// per kernel and launch shape from measurements: loads and stores together speed up the
+// balanced streams (per-event kernels 3-6%, writes 3-7%, cell copies 7%, the copy 16%);
+// read-dominated streams gain from hinted loads alone (gamma and weight gradients,
+// triangular with 7+ updates); hinted loads without hinted stores slow the balanced
+// streams down (1-3%); slices narrower than a 128-byte line take no hint (16-slot
+// read/write with 16+ events: 7-60% slower).
 template <bool NT = false, typename R>
 __device__ __forceinline__ R ld(const R* p) {
   if constexpr (NT) {
@@ -378,11 +400,12 @@ __device__ __forceinline__ void stage_weights(float* lds, const TW* __restrict__
 // read: out_e[m,c] = sum_s alpha[e,c,s] * x[m,s,c]
 // 1-D grid of (slices x chunks), block (BCG, TL); LDS holds alpha as [E][S][BC] fp32.
 // ----------------------------------------------------------------------------------
-template <typename T, int V, int K, int BCGT, bool NTL>
+template <typename T, int V, int K, int BCGT, int NTM>
 __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict__ x, const T* __restrict__ alpha,
                                               PtrPack out, const int32_t* __restrict__ index,
                                               int E, Geo g, int tpb, int nslices) {
   constexpr int S = K * K;
+  constexpr bool NTL = (NTM & 1) != 0, NTS = (NTM & 2) != 0;  // hints: loads, stores
   // tokens per lane per iteration: each LDS weight feeds U tokens
   constexpr int U = K == 2 ? SIHC_RW_UNROLL : SIHC_RW_UNROLL_K4;
   extern __shared__ float lds[];
@@ -428,7 +451,7 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict_
       T* dst = static_cast<T*>(const_cast<void*>(out.p[e]));
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        if (ok[u]) store_vec<T, V>(dst + zoff[u], acc[u]);
+        if (ok[u]) store_vec<T, V, NTS>(dst + zoff[u], acc[u]);
     }
   }
 }
@@ -438,12 +461,13 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict_
 // Events are consumed in groups of 4 (E padded to a multiple of 4 with zero weights
 // and a repeated valid pointer), so each group's 4 update loads issue together.
 // ----------------------------------------------------------------------------------
-template <typename TX, typename TW, int V, int K, bool ADD_X, int BCGT, bool NTL>
+template <typename TX, typename TW, int V, int K, bool ADD_X, int BCGT, int NTM>
 __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restrict__ x, PtrPack upd,
                                                const TW* __restrict__ beta, TX* __restrict__ out,
                                                const int32_t* __restrict__ index, int E, Geo g, int tpb,
                                                int nslices) {
   constexpr int S = K * K;
+  constexpr bool NTL = (NTM & 1) != 0, NTS = (NTM & 2) != 0;  // hints: loads, stores
   // tokens per lane per iteration: each LDS weight feeds U tokens
   constexpr int U = K == 2 ? SIHC_RW_UNROLL : SIHC_RW_UNROLL_K4;
   constexpr int EG = U > 1 ? 2 : 4;  // events per load group
@@ -529,7 +553,7 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restric
     for (int u = 0; u < U; ++u)
       if (ok[u]) {
 #pragma unroll
-        for (int s = 0; s < S; ++s) store_vec<TX, V>(out + slot_offset<K>(p0[u], s, g, c0), acc[u][s]);
+        for (int s = 0; s < S; ++s) store_vec<TX, V, NTS>(out + slot_offset<K>(p0[u], s, g, c0), acc[u][s]);
       }
   }
 }
@@ -572,7 +596,11 @@ __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack 
                                                const int32_t* __restrict__ index, int E, Geo g, int tpb,
                                                int nslices, int TT, PtrPack dout, const void* __restrict__ gam,
                                                int gam_f32) {
-  constexpr bool NTL = !STORE_D;  // non-temporal loads, except in the fused triangular backward
+  // non-temporal loads; the fused triangular backward (3+ updates here) also hints its
+  // update-gradient stores (1-2% faster than either alone)
+  constexpr int HM = SIHC_TRIB_NTM >= 0 ? SIHC_TRIB_NTM : 3;
+  constexpr bool NTL = STORE_D ? (HM & 1) != 0 : true;
+  constexpr bool NTS = STORE_D && (HM & 2) != 0;
   constexpr int S = CARRIER ? K * K : 1;
   static_assert(!(STORE_D && CARRIER), "update gradients exist only in workspace mode");
   extern __shared__ float xt[];  // [TT*S rows][BCG*V], lds_w layout
@@ -667,7 +695,7 @@ __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack 
               float d[V];
 #pragma unroll
               for (int v = 0; v < V; ++v) d[v] = xt[lds_w<V>(t + q, cg, v, BCG)] * gv[v];
-              store_vec<T, V>(de + int64_t(t0 + t + q) * g.C + c0, d);
+              store_vec<T, V, NTS>(de + int64_t(t0 + t + q) * g.C + c0, d);
             }
           }
         }
@@ -691,12 +719,15 @@ __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack 
 // LDS or barriers. Workspace mode and the 4-slot carrier only (16-slot accumulators
 // would not fit the registers beside TG tokens of x).
 // ----------------------------------------------------------------------------------
-template <typename T, int V, int K, bool CARRIER, bool STORE_D>
+template <typename T, int V, int K, bool CARRIER, bool STORE_D, int HM>
 __global__ void __launch_bounds__(256) k_wgrad_direct(const T* __restrict__ x, PtrPack z, float* __restrict__ part,
                                                       const int32_t* __restrict__ index, int E, Geo g, int tpb,
                                                       int nslices, PtrPack dout, const void* __restrict__ gam,
                                                       int gam_f32) {
-  constexpr bool NTL = true;
+  // hint mode HM (bit 0 loads, bit 1 stores) applies to the fused triangular backward;
+  // the plain weight gradients hint their loads
+  constexpr bool NTL = STORE_D ? (HM & 1) != 0 : true;
+  constexpr bool NTS = STORE_D && (HM & 2) != 0;
   constexpr int S = CARRIER ? K * K : 1;
   constexpr int TG = CARRIER ? 2 : 4;
   static_assert(!(STORE_D && CARRIER), "update gradients exist only in workspace mode");
@@ -749,7 +780,7 @@ __global__ void __launch_bounds__(256) k_wgrad_direct(const T* __restrict__ x, P
           float d[V];
 #pragma unroll
           for (int v = 0; v < V; ++v) d[v] = xv[q][0][v] * gv[v];
-          store_vec<T, V>(de + int64_t(m0 + q) * g.C + c0, d);
+          store_vec<T, V, NTS>(de + int64_t(m0 + q) * g.C + c0, d);
         }
       }
     }
@@ -1068,10 +1099,11 @@ __global__ void __launch_bounds__(256) k_fill_zero(TO* __restrict__ out, int64_t
 // triangular: out[m,c] = base[m,c] + sum_j gamma[j,c] * upd_j[m,c]
 // (active count padded to a multiple of 4 with zero gamma rows, as in k_write)
 // ----------------------------------------------------------------------------------
-template <typename T, typename TG, int V, bool NTL>
+template <typename T, typename TG, int V, int NTM>
 __global__ void __launch_bounds__(256) k_triangular(const T* __restrict__ base, PtrPack upd,
                                                     const TG* __restrict__ gamma, T* __restrict__ out,
                                                     int A, int M, int C, int tpb, int nslices) {
+  constexpr bool NTL = (NTM & 1) != 0, NTS = (NTM & 2) != 0;  // hints: loads, stores
   constexpr int U = SIHC_RW_UNROLL;  // tokens per lane per iteration: each LDS weight feeds U tokens
   extern __shared__ float lds[];
   const int BCG = blockDim.x, TL = blockDim.y;
@@ -1127,7 +1159,7 @@ __global__ void __launch_bounds__(256) k_triangular(const T* __restrict__ base, 
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
-      if (ok[u]) store_vec<T, V>(out + off[u], acc[u]);
+      if (ok[u]) store_vec<T, V, NTS>(out + off[u], acc[u]);
   }
 }
 
@@ -1353,17 +1385,20 @@ __global__ void __launch_bounds__(256) k_cells(const R* __restrict__ src, R* __r
   const int64_t xrow = pix * row_chunks;
   const int64_t crow = row * row_chunks;
   for (int i = threadIdx.x; i < row_chunks; i += blockDim.x) {
+    constexpr bool NTL = (SIHC_CELLS_NTM & 1) != 0, NTS = (SIHC_CELLS_NTM & 2) != 0;
     if constexpr (GATHER) {
-      dst[crow + i] = src[xrow + i];
+      st<NTS>(dst + crow + i, ld<NTL>(src + xrow + i));
     } else {
-      dst[xrow + i] = src[crow + i];
+      st<NTS>(dst + xrow + i, ld<NTL>(src + crow + i));
     }
   }
 }
 
 __global__ void __launch_bounds__(256) k_copy16(const u32x4* __restrict__ src, u32x4* __restrict__ dst, int64_t n) {
   const int64_t stride = int64_t(gridDim.x) * blockDim.x;
-  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) st(dst + i, ld(src + i));
+  constexpr bool NTL = (SIHC_COPY_NTM & 1) != 0, NTS = (SIHC_COPY_NTM & 2) != 0;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+    st<NTS>(dst + i, ld<NTL>(src + i));
 }
 
 __global__ void k_copy1(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t n) {
@@ -1604,6 +1639,40 @@ int with_bool(bool b, F&& f) {
   return f(std::false_type{});
 }
 
+// Non-temporal hint mode of a stage kernel: bit 0 loads, bit 1 stores. A compile-time
+// FORCED >= 0 instantiates that mode only.
+template <int FORCED, typename F>
+int with_hints(int mode, F&& f) {
+  if constexpr (FORCED >= 0) {
+    (void)mode;
+    return f(IC<FORCED>{});
+  } else {
+    switch (mode) {
+      case 1: return f(IC<1>{});
+      case 2: return f(IC<2>{});
+      case 3: return f(IC<3>{});
+      default: return f(IC<0>{});
+    }
+  }
+}
+
+// Hint modes of the stage kernels, measured per launch shape at batch 256, D 1152, bf16
+// (all modes give identical results). Slices narrower than a 128-byte line take no hint
+// (16-slot cells with 16+ events: loads or stores hinted run 7-60% slower).
+int read_hints(bool whole_line, int cell, int events) {
+  if (!whole_line) return 0;
+  if (events == 1) return 1;                       // read-dominated (S rows in, 1 out)
+  if (events <= (cell == 2 ? 8 : 12)) return 3;    // 2-5% faster than loads only / none
+  return cell == 2 ? 2 : 0;                        // write-dominated: stores only (0-1.5%)
+}
+int write_hints(bool whole_line, int events) {
+  if (!whole_line) return 0;
+  return events <= 2 ? 2 : 3;  // E <= 2: stores only (4-5%); more events: both (3-7%)
+}
+int triangular_hints(int active) {
+  return active <= 2 ? 2 : active <= 6 ? 3 : 1;  // stores, both, then loads only (A >= 12: both +4%)
+}
+
 // 1-D grid of slices x chunks (slices fastest: concurrently resident blocks cover whole
 // channel rows of a token range).
 unsigned blocks1d(int slices, int64_t chunks) { return unsigned(int64_t(slices) * chunks); }
@@ -1774,9 +1843,21 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
             else goz(IC<2>{}, IC<1>{}, IC<2>{}, nw);
           } else {
             if (events <= 2) {
-              hipLaunchKernelGGL((k_wgrad_direct<T, VV, KK, CAR, SD>), dim3(blocks1d(slices, chunks)),
-                                 dim3(bcg, events), 0, st, static_cast<const T*>(x), pk, part, index, events, g,
-                                 tpb, slices, dk, gamma, gf32);
+              // fused triangular backward: 1 update hints loads only, 2 updates stores
+              // only (11% faster than loads only at the XL shape)
+              auto direct = [&](auto h) {
+                constexpr int HM = decltype(h)::value;
+                hipLaunchKernelGGL((k_wgrad_direct<T, VV, KK, CAR, SD, HM>), dim3(blocks1d(slices, chunks)),
+                                   dim3(bcg, events), 0, st, static_cast<const T*>(x), pk, part, index, events, g,
+                                   tpb, slices, dk, gamma, gf32);
+              };
+              if constexpr (SIHC_TRIB_NTM >= 0) {
+                direct(IC<SIHC_TRIB_NTM>{});
+              } else if (SD && events == 2) {
+                direct(IC<2>{});
+              } else {
+                direct(IC<1>{});
+              }
             } else {
               hipLaunchKernelGGL((k_wgrad<T, VV, KK, CAR, SD>), dim3(blocks1d(slices, chunks)), dim3(bcg, events),
                                  lds, st, static_cast<const T*>(x), pk, part, index, events, g, tpb, slices, tt, dk,
@@ -1849,11 +1930,11 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
           } else {
             // non-temporal carrier loads: for 1-2 events (4 slots) or up to 12 (16 slots),
             // and only with slice rows of whole 128-byte lines
-            const bool ntl = sh.bcg * VV * int(sizeof(T)) >= 128 && events <= (KK == 2 ? 2 : 12);
+            const int hints = read_hints(sh.bcg * VV * int(sizeof(T)) >= 128, cell, events);
             return with_bcg<KK>(sh.bcg, [&](auto bb) {
               constexpr int BB = decltype(bb)::value;
-              return with_bool(ntl, [&](auto nt) {
-                constexpr bool NT = decltype(nt)::value;
+              return with_hints<SIHC_RD_NTM>(hints, [&](auto nt) {
+                constexpr int NT = decltype(nt)::value;
                 hipLaunchKernelGGL((k_read<T, VV, KK, BB, NT>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl),
                                    lds, st, static_cast<const T*>(x), static_cast<const T*>(alpha), pk, index, events,
                                    g, tpb, sh.slices);
@@ -1909,13 +1990,13 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
             return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
           } else {
             // non-temporal loads with 8+ events and slice rows of whole 128-byte lines
-            const bool ntl = sh.bcg * VV * int(sizeof(TX)) >= 128 && events >= 8;
+            const int hints = write_hints(sh.bcg * VV * int(sizeof(TX)) >= 128, events);
             return with_bool(add_x != 0, [&](auto ax) {
               constexpr bool AX = decltype(ax)::value;
               return with_bcg<KK>(sh.bcg, [&](auto bb) {
                 constexpr int BB = decltype(bb)::value;
-                return with_bool(ntl, [&](auto nt) {
-                  constexpr bool NT = decltype(nt)::value;
+                return with_hints<SIHC_WR_NTM>(hints, [&](auto nt) {
+                  constexpr int NT = decltype(nt)::value;
                   hipLaunchKernelGGL((k_write<TX, TW, VV, KK, AX, BB, NT>), dim3(blocks1d(sh.slices, chunks)),
                                      dim3(sh.bcg, sh.tl), lds, st, static_cast<const TX*>(x), pk,
                                      static_cast<const TW*>(beta), static_cast<TX*>(out), index, events, g, tpb,
@@ -1989,9 +2070,8 @@ int sihc_triangular(const void* base, const void* const* updates, const void* ga
         if constexpr (VV * sizeof(T) > 16) {
           return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
         } else {
-          // non-temporal loads with 3+ updates (read-dominated: (A + 1) rows in, 1 out)
-          return with_bool(active >= 3, [&](auto nt) {
-            constexpr bool NT = decltype(nt)::value;
+          return with_hints<SIHC_TRI_NTM>(triangular_hints(active), [&](auto nt) {
+            constexpr int NT = decltype(nt)::value;
             hipLaunchKernelGGL((k_triangular<T, TG, VV, NT>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl),
                                lds, st, static_cast<const T*>(base), pk, static_cast<const TG*>(gamma),
                                static_cast<T*>(out), active, int(rows), channels, tpb, sh.slices);
