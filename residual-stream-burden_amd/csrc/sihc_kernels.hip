@@ -48,7 +48,7 @@
 #define SIHC_EV_BCG 32
 #endif
 #ifndef SIHC_EV_TPT  // tokens per lane, per-event forward
-#define SIHC_EV_TPT 4
+#define SIHC_EV_TPT 2
 #endif
 #ifndef SIHC_EV_UNROLL  // tokens per lane per loop iteration, per-event kernels
 #define SIHC_EV_UNROLL 2
@@ -60,7 +60,10 @@
 #define SIHC_EV_CHUNK 256
 #endif
 #ifndef SIHC_EV_GROUP  // tokens per interleaved group of a backward chunk (0: contiguous)
-#define SIHC_EV_GROUP 64
+#define SIHC_EV_GROUP 32
+#endif
+#ifndef SIHC_EV_GROUP_K4  // the same for 16-slot cells
+#define SIHC_EV_GROUP_K4 64
 #endif
 #ifndef SIHC_EV_BWD_NT  // non-temporal hints in the per-event backward: 1 loads, 2 stores, 3 both
 #define SIHC_EV_BWD_NT 3
@@ -2258,7 +2261,8 @@ int sihc_event_backward(const void* grad_x_out, const void* grad_z_out, const vo
               chunks = whole_rounds(sh.slices, max_chunks, resident_blocks(kfn, sh.bcg * sh.tl, lds));
               // token groups: a multiple of one loop iteration (SIHC_EV_UNROLL x TL tokens);
               // group 0 means one contiguous run of tokens per chunk
-              const int gs = group_tokens(SIHC_EV_GROUP, g.M, chunks, SIHC_EV_UNROLL * sh.tl);
+              const int gs = group_tokens(KK == 2 ? SIHC_EV_GROUP : SIHC_EV_GROUP_K4, g.M, chunks,
+                                          SIHC_EV_UNROLL * sh.tl);
               hipLaunchKernelGGL((k_event_bwd<T, VV, KK, HH, HG, HW, STT, NTL, NTS>), dim3(blocks1d(sh.slices, chunks)),
                                  dim3(sh.bcg, sh.tl), lds, st, static_cast<const T*>(grad_x_out),
                                  static_cast<const T*>(grad_z_out), static_cast<const T*>(x_out),
