@@ -97,7 +97,7 @@
 #ifndef SIHC_RW_UNROLL  // tokens per lane per loop iteration, read / write / triangular
 #define SIHC_RW_UNROLL 2
 #endif
-#ifndef SIHC_RW_TPT  // tokens per lane, read / write / triangular
+#ifndef SIHC_RW_TPT  // tokens per lane, write (4-slot cells) and 16-slot read / write with few events
 #define SIHC_RW_TPT 8
 #endif
 // 16-slot cells: a lane holds 16 slot vectors per token and reads 16 weights per event
@@ -406,7 +406,7 @@ __device__ __forceinline__ void stage_weights(float* lds, const TW* __restrict__
 template <typename T, int V, int K, int BCGT, int NTM>
 __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict__ x, const T* __restrict__ alpha,
                                               PtrPack out, const int32_t* __restrict__ index,
-                                              int E, Geo g, int tpb, int nslices) {
+                                              int E, Geo g, int gs, int nchunks, int nslices) {
   constexpr int S = K * K;
   constexpr bool NTL = (NTM & 1) != 0, NTS = (NTM & 2) != 0;  // hints: loads, stores
   // tokens per lane per iteration: each LDS weight feeds U tokens
@@ -421,16 +421,19 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict_
   stage_weights<V>(lds, alpha, E, E, S, BCG, cs, g.C);
   const int c0 = cs + threadIdx.x * V;
   if (c0 >= g.C) return;
-  const int m_begin = chunk * tpb;
-  const int m_end = min(m_begin + tpb, g.M);
-  for (int m = m_begin + threadIdx.y; m < m_end; m += U * TL) {
+  // The block's tokens: groups of gs tokens (a multiple of U * TL), group `chunk` and
+  // every nchunks-th one after it (the launchers pass gs = the block's whole run).
+  for (int64_t m0 = int64_t(chunk) * gs; m0 < g.M; m0 += int64_t(nchunks) * gs) {
+   const int64_t m_end = min(m0 + gs, int64_t(g.M));
+   for (int64_t mi = m0; mi < m_end; mi += U * TL) {
+    const int64_t m = mi + threadIdx.y;
     bool ok[U];
     int64_t zoff[U];
     float xv[U][S][V];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       ok[u] = m + u * TL < m_end;
-      const int mu = ok[u] ? m + u * TL : m;  // tail: reload a valid token, store nothing
+      const int mu = int(ok[u] ? m + u * TL : mi);  // tail: reload a valid token, store nothing
       const int64_t p0 = cell_pixel0(mu, g, index);
       zoff[u] = int64_t(mu) * g.C + c0;
 #pragma unroll
@@ -457,6 +460,7 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict_
         if (ok[u]) store_vec<T, V, NTS>(dst + zoff[u], acc[u]);
     }
   }
+  }
 }
 
 // ----------------------------------------------------------------------------------
@@ -467,8 +471,8 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict_
 template <typename TX, typename TW, int V, int K, bool ADD_X, int BCGT, int NTM>
 __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restrict__ x, PtrPack upd,
                                                const TW* __restrict__ beta, TX* __restrict__ out,
-                                               const int32_t* __restrict__ index, int E, Geo g, int tpb,
-                                               int nslices) {
+                                               const int32_t* __restrict__ index, int E, Geo g, int gs,
+                                               int nchunks, int nslices) {
   constexpr int S = K * K;
   constexpr bool NTL = (NTM & 1) != 0, NTS = (NTM & 2) != 0;  // hints: loads, stores
   // tokens per lane per iteration: each LDS weight feeds U tokens
@@ -483,16 +487,19 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restric
   stage_weights<V>(lds, beta, E, E4, S, BCG, cs, g.C);
   const int c0 = cs + threadIdx.x * V;
   if (c0 >= g.C) return;
-  const int m_begin = chunk * tpb;
-  const int m_end = min(m_begin + tpb, g.M);
-  for (int m = m_begin + threadIdx.y; m < m_end; m += U * TL) {
+  // The block's tokens: groups of gs tokens (a multiple of U * TL), group `chunk` and
+  // every nchunks-th one after it (the launchers pass gs = the block's whole run).
+  for (int64_t m0 = int64_t(chunk) * gs; m0 < g.M; m0 += int64_t(nchunks) * gs) {
+   const int64_t m_end = min(m0 + gs, int64_t(g.M));
+   for (int64_t mi = m0; mi < m_end; mi += U * TL) {
+    const int64_t m = mi + threadIdx.y;
     bool ok[U];
     int64_t p0[U], zoff[U];
     float acc[U][S][V];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       ok[u] = m + u * TL < m_end;
-      const int mu = ok[u] ? m + u * TL : m;  // tail: reload a valid token, store nothing
+      const int mu = int(ok[u] ? m + u * TL : mi);  // tail: reload a valid token, store nothing
       p0[u] = cell_pixel0(mu, g, index);
       zoff[u] = int64_t(mu) * g.C + c0;
       if constexpr (ADD_X) {
@@ -558,6 +565,7 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restric
 #pragma unroll
         for (int s = 0; s < S; ++s) store_vec<TX, V, NTS>(out + slot_offset<K>(p0[u], s, g, c0), acc[u][s]);
       }
+  }
   }
 }
 
@@ -1105,7 +1113,7 @@ __global__ void __launch_bounds__(256) k_fill_zero(TO* __restrict__ out, int64_t
 template <typename T, typename TG, int V, int NTM>
 __global__ void __launch_bounds__(256) k_triangular(const T* __restrict__ base, PtrPack upd,
                                                     const TG* __restrict__ gamma, T* __restrict__ out,
-                                                    int A, int M, int C, int tpb, int nslices) {
+                                                    int A, int M, int C, int gs, int nchunks, int nslices) {
   constexpr bool NTL = (NTM & 1) != 0, NTS = (NTM & 2) != 0;  // hints: loads, stores
   constexpr int U = SIHC_RW_UNROLL;  // tokens per lane per iteration: each LDS weight feeds U tokens
   extern __shared__ float lds[];
@@ -1125,16 +1133,19 @@ __global__ void __launch_bounds__(256) k_triangular(const T* __restrict__ base, 
   __syncthreads();
   const int c0 = cs + threadIdx.x * V;
   if (c0 >= C) return;
-  const int m_begin = chunk * tpb;
-  const int m_end = min(m_begin + tpb, M);
-  for (int m = m_begin + threadIdx.y; m < m_end; m += U * TL) {
+  // The block's tokens: groups of gs tokens (a multiple of U * TL), group `chunk` and
+  // every nchunks-th one after it (the launchers pass gs = the block's whole run).
+  for (int64_t m0 = int64_t(chunk) * gs; m0 < M; m0 += int64_t(nchunks) * gs) {
+   const int64_t m_end = min(m0 + gs, int64_t(M));
+   for (int64_t mi = m0; mi < m_end; mi += U * TL) {
+    const int64_t m = mi + threadIdx.y;
     bool ok[U];
     int64_t off[U];
     float acc[U][V];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       ok[u] = m + u * TL < m_end;
-      off[u] = int64_t(ok[u] ? m + u * TL : m) * C + c0;
+      off[u] = (ok[u] ? m + u * TL : mi) * C + c0;
       load_vec<T, V, NTL>(base + off[u], acc[u]);
     }
     for (int j = 0; j < A4; j += 4) {
@@ -1163,6 +1174,7 @@ __global__ void __launch_bounds__(256) k_triangular(const T* __restrict__ base, 
 #pragma unroll
     for (int u = 0; u < U; ++u)
       if (ok[u]) store_vec<T, V, NTS>(out + off[u], acc[u]);
+  }
   }
 }
 
@@ -1469,8 +1481,10 @@ Shape2D shape_for(int C, int V, int bcg0, int lds_per_channel, int lds_cap = 64 
 // into LDS; with 16-slot cells that staging is large enough that blocks must cover more
 // tokens as E grows (measured at batch 256, D 1152: E = 24 read 1872 -> 1624 us with
 // 64 tokens per lane, while E = 1 is fastest with 8).
-int rw_tokens_per_lane(int cell, int events) {
-  if (cell == 2) return SIHC_RW_TPT;
+int rw_tokens_per_lane(int cell, int events, bool read = false) {
+  // 4-slot reads: 32-token blocks (64 with one event) stream through a narrower window
+  // than 128-token ones (E = 2..16: 6-7% faster)
+  if (cell == 2) return read ? (events == 1 ? 4 : 2) : SIHC_RW_TPT;
   return events <= 4 ? SIHC_RW_TPT : events <= 16 ? 16 : 64;
 }
 
@@ -1915,8 +1929,9 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
   const int S = cell * cell;
   const Shape2D sh = cell == 2 ? shape_for(channels, V, SIHC_RW_BCG, events * S * 4)
                                : shape_for(channels, V, SIHC_RW_BCG_K4, events * S * 4, SIHC_RW_LDS_K4);
-  const int tpb = sh.tl * rw_tokens_per_lane(cell, events);
+  const int tpb = sh.tl * rw_tokens_per_lane(cell, events, true);
   const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
+  const int gs = tpb;  // one contiguous run per block (interleaved groups measured no faster)
   const size_t lds = size_t(events) * S * sh.bcg * V * 4;
   const PtrPack pk = pack(ptrs, events);
   return with_dtype(dtype, [&](auto t) {
@@ -1940,7 +1955,7 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
                 constexpr int NT = decltype(nt)::value;
                 hipLaunchKernelGGL((k_read<T, VV, KK, BB, NT>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl),
                                    lds, st, static_cast<const T*>(x), static_cast<const T*>(alpha), pk, index, events,
-                                   g, tpb, sh.slices);
+                                   g, gs, int(chunks), sh.slices);
                 return check_launch(what);
               });
             });
@@ -1977,6 +1992,7 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
                                : shape_for(channels, V, SIHC_RW_BCG_K4, E4 * S * 4, SIHC_RW_LDS_K4);
   const int tpb = sh.tl * rw_tokens_per_lane(cell, E4);
   const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
+  const int gs = tpb;  // one contiguous run per block (interleaved groups measured no faster)
   const size_t lds = size_t(E4) * S * sh.bcg * V * 4;
   const PtrPack pk = pack(updates, events);
   auto launch = [&](auto tx, auto tw) {
@@ -2002,7 +2018,8 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
                   constexpr int NT = decltype(nt)::value;
                   hipLaunchKernelGGL((k_write<TX, TW, VV, KK, AX, BB, NT>), dim3(blocks1d(sh.slices, chunks)),
                                      dim3(sh.bcg, sh.tl), lds, st, static_cast<const TX*>(x), pk,
-                                     static_cast<const TW*>(beta), static_cast<TX*>(out), index, events, g, tpb,
+                                     static_cast<const TW*>(beta), static_cast<TX*>(out), index, events, g, gs,
+                                     int(chunks),
                                      sh.slices);
                   return check_launch(what);
                 });
@@ -2059,8 +2076,10 @@ int sihc_triangular(const void* base, const void* const* updates, const void* ga
   const int V = pick_vec(channels, es, 8, ptrs, active + 2);
   const int A4 = (active + 3) & ~3;
   const Shape2D sh = shape_for(channels, V, SIHC_RW_BCG, A4 * 4);
-  const int tpb = sh.tl * SIHC_RW_TPT;
+  // 32-token blocks (64 with one update): 3-5% faster than 128-token ones
+  const int tpb = sh.tl * (active == 1 ? 4 : 2);
   const int64_t chunks = (rows + tpb - 1) / tpb;
+  const int gs = tpb;  // one contiguous run per block
   const size_t lds = size_t(A4) * sh.bcg * V * 4;
   const PtrPack pk = pack(updates, active);
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -2077,7 +2096,7 @@ int sihc_triangular(const void* base, const void* const* updates, const void* ga
             constexpr int NT = decltype(nt)::value;
             hipLaunchKernelGGL((k_triangular<T, TG, VV, NT>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl),
                                lds, st, static_cast<const T*>(base), pk, static_cast<const TG*>(gamma),
-                               static_cast<T*>(out), active, int(rows), channels, tpb, sh.slices);
+                               static_cast<T*>(out), active, int(rows), channels, gs, int(chunks), sh.slices);
             return check_launch(what);
           });
         }
