@@ -1485,6 +1485,11 @@ int rw_tokens_per_lane(int cell, int events, bool read = false) {
   // 4-slot reads: 32-token blocks (64 with one event) stream through a narrower window
   // than 128-token ones (E = 2..16: 6-7% faster)
   if (cell == 2) return read ? (events == 1 ? 4 : 2) : SIHC_RW_TPT;
+  // 16 slots: the weight slice staged per block grows with E, so blocks grow too; with
+  // hinted loads and stores reads with 3-12 events and writes with 9-12 gain from twice
+  // the tokens again (read E = 8: 794 -> 745 us), 1-2 and 13+ events do not
+  if (read && events >= 3 && events <= 12) return events <= 4 ? 16 : 32;
+  if (!read && events > 8 && events <= 12) return 32;
   return events <= 4 ? SIHC_RW_TPT : events <= 16 ? 16 : 64;
 }
 
