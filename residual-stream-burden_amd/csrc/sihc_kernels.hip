@@ -118,6 +118,9 @@
 #ifndef SIHC_WG_CHUNK  // tokens per reduction chunk, weight / gamma gradients
 #define SIHC_WG_CHUNK 512
 #endif
+#ifndef SIHC_TRIB_CHUNK  // tokens per reduction chunk, fused triangular backward
+#define SIHC_TRIB_CHUNK 64
+#endif
 #ifndef SIHC_WG_TT  // most tokens per staged LDS tile of the weight / gamma gradients
 #define SIHC_WG_TT 32
 #endif
@@ -1527,6 +1530,14 @@ int wgrad_chunks(int64_t M, int events, int C) {
   return int(std::max<int64_t>(base, std::min(want, cap)));
 }
 int event_bwd_chunks(int64_t M) { return chunk_count(M, SIHC_EV_CHUNK, 512); }
+// Token chunks of the fused triangular backward (which also stores the update
+// gradients): one per SIHC_TRIB_CHUNK tokens up to 1024, at least the weight-gradient
+// count. Shorter runs per block stream through a narrower window of each array (A = 3:
+// 269 -> 234 us, A = 11: 731 -> 682 us at the XL shape); the read-only gradients keep
+// their longer chunks, which shorter ones slow down (fewer tokens per partial row).
+int trib_chunks(int64_t M, int events, int C) {
+  return std::max(wgrad_chunks(M, events, C), chunk_count(M, SIHC_TRIB_CHUNK, 1024));
+}
 
 // Tokens per interleaved group of a reduction chunk (chunk c takes groups c, c + chunks,
 // ...): `want` rounded up to a multiple of `step` (the tokens of one loop iteration or
@@ -1768,7 +1779,7 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
                  int S, bool carrier, const int32_t* index, int dtype, int out_dtype, void* workspace,
                  size_t workspace_bytes, hipStream_t st, void* const* dout = nullptr, const void* gamma = nullptr,
                  int gamma_dtype = SIHC_DTYPE_F32) {
-  const int max_chunks = wgrad_chunks(g.M, events, g.C);
+  const int max_chunks = dout ? trib_chunks(g.M, events, g.C) : wgrad_chunks(g.M, events, g.C);
   int chunks = max_chunks;  // k_wgradz may use fewer (whole rounds of resident blocks)
   const size_t need = size_t(max_chunks) * events * S * g.C * sizeof(float);
   if (!workspace || workspace_bytes < need)
@@ -2112,7 +2123,8 @@ int sihc_triangular(const void* base, const void* const* updates, const void* ga
 
 size_t sihc_triangular_gamma_grad_workspace_size(int active, int64_t rows, int channels) {
   if (active < 1 || rows < 0 || channels <= 0) return 0;
-  return size_t(wgrad_chunks(rows, active, channels)) * active * channels * sizeof(float);
+  // covers both users: the gamma gradient and the fused triangular backward (more chunks)
+  return size_t(trib_chunks(rows, active, channels)) * active * channels * sizeof(float);
 }
 
 int sihc_triangular_gamma_grad(const void* grad, const void* const* updates, void* out, int active, int64_t rows,

@@ -38,6 +38,9 @@ def test_workspace_sizes_are_pure_functions_of_sizes():
     # few event lanes: more chunks (about 16 waves per CU), at least 32 tokens each
     assert lib.sihc_triangular_gamma_grad_workspace_size(3, 147, 67) == 4 * 3 * 67 * 4
     assert lib.sihc_triangular_gamma_grad_workspace_size(1, 65536, 1152) == 1366 * 1 * 1152 * 4
+    # the query also covers the fused triangular backward: one chunk per 64 tokens, at
+    # most 1024 (more than the 152 chunks the 11-update gamma gradient takes)
+    assert lib.sihc_triangular_gamma_grad_workspace_size(11, 65536, 1152) == 1024 * 11 * 1152 * 4
     assert lib.sihc_event_backward_workspace_size(256, 16, 2, 1152) == 256 * 2 * 4 * 1152 * 4
 
 
