@@ -118,6 +118,9 @@
 #ifndef SIHC_WG_CHUNK  // tokens per reduction chunk, weight / gamma gradients
 #define SIHC_WG_CHUNK 512
 #endif
+#ifndef SIHC_WG_PAD  // most idle event lanes added to make k_wgrad blocks 4 whole waves
+#define SIHC_WG_PAD 4
+#endif
 #ifndef SIHC_TRIB_CHUNK  // tokens per reduction chunk, fused triangular backward
 #define SIHC_TRIB_CHUNK 64
 #endif
@@ -622,9 +625,11 @@ __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack 
   const int BC = BCG * V;
   const int blk = logical_block<false>(), slice = blk % nslices, chunk = blk / nslices;
   const int cs = slice * BC;
-  const int cg = threadIdx.x, e = threadIdx.y;
+  const int cg = threadIdx.x;
+  // event lanes past E (padding to whole 4-wave blocks) only help stage the tile
+  const int e = min(int(threadIdx.y), E - 1);
   const int c0 = cs + cg * V;
-  const bool active = c0 < g.C;
+  const bool active = c0 < g.C && int(threadIdx.y) < E;
   const T* __restrict__ ze = static_cast<const T*>(z.p[e]);
   const int tid = threadIdx.y * BCG + threadIdx.x;
   const int nthr = BCG * blockDim.y;
@@ -1803,6 +1808,14 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
   int tt = 32768 / (S * bcg * V * int(sizeof(float)));
   tt = std::max(1, std::min(tt, carrier && events <= 16 ? 8 : SIHC_WG_TT));
   const size_t lds = size_t(tt) * S * bcg * V * sizeof(float);
+  // event lanes of k_wgrad: padded so the block is a whole number of 4-wave groups (the
+  // 4 SIMDs of a CU then hold equal shares) where that costs at most SIHC_WG_PAD lanes
+  int lanes = events;
+  if (SIHC_WG_PAD > 0) {
+    int pad = events;
+    while ((bcg * pad) % 256 != 0 && bcg * pad < 256) ++pad;
+    if ((bcg * pad) % 256 == 0 && pad - events <= SIHC_WG_PAD) lanes = pad;
+  }
   const PtrPack pk = pack(z, events);
   const PtrPack dk = dout ? pack(const_cast<const void* const*>(dout), events) : PtrPack{};
   // 16-slot carrier: k_wgrad16 (one channel per lane); only x is loaded as vectors
@@ -1892,7 +1905,7 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
                 direct(IC<1>{});
               }
             } else {
-              hipLaunchKernelGGL((k_wgrad<T, VV, KK, CAR, SD>), dim3(blocks1d(slices, chunks)), dim3(bcg, events),
+              hipLaunchKernelGGL((k_wgrad<T, VV, KK, CAR, SD>), dim3(blocks1d(slices, chunks)), dim3(bcg, lanes),
                                  lds, st, static_cast<const T*>(x), pk, part, index, events, g, tpb, slices, tt, dk,
                                  gamma, gf32);
             }
