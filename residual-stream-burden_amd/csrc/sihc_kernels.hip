@@ -10,7 +10,11 @@
 // with stride TL, so each wave issues fully coalesced vector loads, and the per-channel
 // weights of its channel group are fetched once per block: into LDS when the kernel
 // handles many events (read / write / triangular), into registers when it handles one
-// (per-event fused kernels). Every token is processed as "issue all loads, then
+// (per-event fused kernels). Runs are short (16-64 tokens for the per-event forward,
+// read and triangular) or, where a run is one reduction chunk (per-event backward),
+// interleaved groups of 32-64 tokens, so the blocks resident at one time stream through
+// a narrow window of each array; loads and stores carry non-temporal hints where that
+// measured faster. Every token is processed as "issue all loads, then
 // compute, then store" with no data-dependent branches in the loop body, so each lane
 // keeps all of a token's loads in flight at once (the write also issues the next event
 // group's loads early). The pipelined carrier weight gradient instead gives each lane
