@@ -116,6 +116,9 @@
 #ifndef SIHC_RW_BCG_K4  // channel-group lanes per block of k_read / k_write, 16 slots
 #define SIHC_RW_BCG_K4 32
 #endif
+#ifndef SIHC_K4_BF16W  // 1: 16-slot read / write stage bf16 weights packed as bf16 in LDS
+#define SIHC_K4_BF16W 1
+#endif
 #ifndef SIHC_RW_LDS_K4  // LDS bytes per block for staged weights, 16 slots
 #define SIHC_RW_LDS_K4 (48 * 1024)
 #endif
@@ -409,11 +412,45 @@ __device__ __forceinline__ void stage_weights(float* lds, const TW* __restrict__
   __syncthreads();
 }
 
+// bf16 weights with 2-channel lanes (16-slot read / write): the same slice as
+// stage_weights in half the LDS, one 32-bit word per (row, lane) holding the lane's two
+// channels as bf16 (low half: the even channel). Exact: a bf16 weight widens to the same
+// fp32 value either way.
+__device__ __forceinline__ void stage_weights_bf16x2(uint32_t* lds, const bf16_t* __restrict__ w, int E, int Epad,
+                                                     int S, int BCG, int cs, int C) {
+  const int tid = threadIdx.y * blockDim.x + threadIdx.x;
+  const int nthr = blockDim.x * blockDim.y;
+  for (int i = tid; i < Epad * BCG * S; i += nthr) {  // [e][lane][s]
+    const int e = i / (BCG * S);
+    const int r = i - e * BCG * S;
+    const int cg = r / S;
+    const int s = r - cg * S;
+    const int c = cs + 2 * cg;
+    const uint32_t lo = (e < E && c < C) ? uint32_t(w[(int64_t(e) * C + c) * S + s]) : 0u;
+    const uint32_t hi = (e < E && c + 1 < C) ? uint32_t(w[(int64_t(e) * C + c + 1) * S + s]) : 0u;
+    lds[(e * S + s) * BCG + cg] = lo | (hi << 16);
+  }
+  __syncthreads();
+}
+// The V weights of weight row `row` for lane cg from either LDS layout.
+template <int V, bool WB>
+__device__ __forceinline__ void lds_weights(const float* lds, int row, int cg, int BCG, float (&a)[V]) {
+  if constexpr (WB) {
+    static_assert(V == 2, "packed bf16 weights hold 2 channels per lane");
+    const uint32_t w = reinterpret_cast<const uint32_t*>(lds)[row * BCG + cg];
+    a[0] = __uint_as_float(w << 16);
+    a[1] = __uint_as_float(w & 0xffff0000u);
+  } else {
+#pragma unroll
+    for (int v = 0; v < V; ++v) a[v] = lds[lds_w<V>(row, cg, v, BCG)];
+  }
+}
+
 // ----------------------------------------------------------------------------------
 // read: out_e[m,c] = sum_s alpha[e,c,s] * x[m,s,c]
 // 1-D grid of (slices x chunks), block (BCG, TL); LDS holds alpha as [E][S][BC] fp32.
 // ----------------------------------------------------------------------------------
-template <typename T, int V, int K, int BCGT, int NTM>
+template <typename T, int V, int K, int BCGT, int NTM, bool WB>
 __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict__ x, const T* __restrict__ alpha,
                                               PtrPack out, const int32_t* __restrict__ index,
                                               int E, Geo g, int gs, int nchunks, int nslices) {
@@ -428,7 +465,12 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict_
   const int BC = BCG * V;
   const int blk = logical_block<true>(), slice = blk % nslices, chunk = blk / nslices;
   const int cs = slice * BC;
-  stage_weights<V>(lds, alpha, E, E, S, BCG, cs, g.C);
+  if constexpr (WB) {
+    stage_weights_bf16x2(reinterpret_cast<uint32_t*>(lds), reinterpret_cast<const bf16_t*>(alpha), E, E, S, BCG, cs,
+                         g.C);
+  } else {
+    stage_weights<V>(lds, alpha, E, E, S, BCG, cs, g.C);
+  }
   const int c0 = cs + threadIdx.x * V;
   if (c0 >= g.C) return;
   // The block's tokens: groups of gs tokens (a multiple of U * TL), group `chunk` and
@@ -457,13 +499,14 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict_
 #pragma unroll
         for (int v = 0; v < V; ++v) acc[u][v] = 0.f;
 #pragma unroll
-      for (int s = 0; s < S; ++s)
+      for (int s = 0; s < S; ++s) {
+        float a[V];
+        lds_weights<V, WB>(lds, e * S + s, threadIdx.x, BCG, a);
 #pragma unroll
-        for (int v = 0; v < V; ++v) {
-          const float a = lds[lds_w<V>(e * S + s, threadIdx.x, v, BCG)];
+        for (int v = 0; v < V; ++v)
 #pragma unroll
-          for (int u = 0; u < U; ++u) acc[u][v] = fmaf(a, xv[u][s][v], acc[u][v]);
-        }
+          for (int u = 0; u < U; ++u) acc[u][v] = fmaf(a[v], xv[u][s][v], acc[u][v]);
+      }
       T* dst = static_cast<T*>(const_cast<void*>(out.p[e]));
 #pragma unroll
       for (int u = 0; u < U; ++u)
@@ -478,7 +521,7 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict_
 // Events are consumed in groups of 4 (E padded to a multiple of 4 with zero weights
 // and a repeated valid pointer), so each group's 4 update loads issue together.
 // ----------------------------------------------------------------------------------
-template <typename TX, typename TW, int V, int K, bool ADD_X, int BCGT, int NTM>
+template <typename TX, typename TW, int V, int K, bool ADD_X, int BCGT, int NTM, bool WB>
 __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restrict__ x, PtrPack upd,
                                                const TW* __restrict__ beta, TX* __restrict__ out,
                                                const int32_t* __restrict__ index, int E, Geo g, int gs,
@@ -494,7 +537,12 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restric
   const int blk = logical_block<true>(), slice = blk % nslices, chunk = blk / nslices;
   const int cs = slice * BC;
   const int E4 = (E + 3) & ~3;
-  stage_weights<V>(lds, beta, E, E4, S, BCG, cs, g.C);
+  if constexpr (WB) {
+    stage_weights_bf16x2(reinterpret_cast<uint32_t*>(lds), reinterpret_cast<const bf16_t*>(beta), E, E4, S, BCG, cs,
+                         g.C);
+  } else {
+    stage_weights<V>(lds, beta, E, E4, S, BCG, cs, g.C);
+  }
   const int c0 = cs + threadIdx.x * V;
   if (c0 >= g.C) return;
   // The block's tokens: groups of gs tokens (a multiple of U * TL), group `chunk` and
@@ -561,13 +609,14 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restric
 #pragma unroll
       for (int q = 0; q < EG; ++q)
 #pragma unroll
-        for (int s = 0; s < S; ++s)
+        for (int s = 0; s < S; ++s) {
+          float b[V];
+          lds_weights<V, WB>(lds, (e + q) * S + s, threadIdx.x, BCG, b);
 #pragma unroll
-          for (int v = 0; v < V; ++v) {
-            const float b = lds[lds_w<V>((e + q) * S + s, threadIdx.x, v, BCG)];
+          for (int v = 0; v < V; ++v)
 #pragma unroll
-            for (int u = 0; u < U; ++u) acc[u][s][v] = fmaf(b, dz[q][u][v], acc[u][s][v]);
-          }
+            for (int u = 0; u < U; ++u) acc[u][s][v] = fmaf(b[v], dz[q][u][v], acc[u][s][v]);
+        }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -1704,8 +1753,8 @@ int with_hints(int mode, F&& f) {
 int read_hints(bool whole_line, int cell, int events) {
   if (!whole_line) return 0;
   if (events == 1) return 1;                       // read-dominated (S rows in, 1 out)
-  if (events <= (cell == 2 ? 8 : 12)) return 3;    // 2-5% faster than loads only / none
-  return cell == 2 ? 2 : 0;                        // write-dominated: stores only (0-1.5%)
+  if (cell == 4 || events <= 8) return 3;          // 2-5% faster than loads only / none
+  return 2;                                        // write-dominated: stores only (0-1.5%)
 }
 int write_hints(bool whole_line, int events) {
   if (!whole_line) return 0;
@@ -1960,12 +2009,16 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int V = pick_vec(channels, es, cell == 2 ? 8 : SIHC_RW_VEC_K4, ptrs, events + 1);
   const int S = cell * cell;
+  // 16 slots, bf16 weights, 2-channel lanes: weights packed as bf16 in LDS (half the
+  // bytes, so twice the channels per block within the LDS budget)
+  const bool wb = SIHC_K4_BF16W && cell == 4 && dtype == SIHC_DTYPE_BF16 && V == 2;
+  const int wbytes = wb ? 2 : 4;
   const Shape2D sh = cell == 2 ? shape_for(channels, V, SIHC_RW_BCG, events * S * 4)
-                               : shape_for(channels, V, SIHC_RW_BCG_K4, events * S * 4, SIHC_RW_LDS_K4);
+                               : shape_for(channels, V, SIHC_RW_BCG_K4, events * S * wbytes, SIHC_RW_LDS_K4);
   const int tpb = sh.tl * rw_tokens_per_lane(cell, events, true);
   const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
   const int gs = tpb;  // one contiguous run per block (interleaved groups measured no faster)
-  const size_t lds = size_t(events) * S * sh.bcg * V * 4;
+  const size_t lds = size_t(events) * S * sh.bcg * V * wbytes;
   const PtrPack pk = pack(ptrs, events);
   return with_dtype(dtype, [&](auto t) {
     using T = decltype(t);
@@ -1986,10 +2039,17 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
               constexpr int BB = decltype(bb)::value;
               return with_hints<SIHC_RD_NTM>(hints, [&](auto nt) {
                 constexpr int NT = decltype(nt)::value;
-                hipLaunchKernelGGL((k_read<T, VV, KK, BB, NT>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl),
-                                   lds, st, static_cast<const T*>(x), static_cast<const T*>(alpha), pk, index, events,
-                                   g, gs, int(chunks), sh.slices);
-                return check_launch(what);
+                auto go = [&](auto w) {
+                  constexpr bool WB = decltype(w)::value;
+                  hipLaunchKernelGGL((k_read<T, VV, KK, BB, NT, WB>), dim3(blocks1d(sh.slices, chunks)),
+                                     dim3(sh.bcg, sh.tl), lds, st, static_cast<const T*>(x),
+                                     static_cast<const T*>(alpha), pk, index, events, g, gs, int(chunks), sh.slices);
+                  return check_launch(what);
+                };
+                if constexpr (KK == 4 && VV == 2 && std::is_same_v<T, bf16_t>) {
+                  if (wb) return go(std::true_type{});
+                }
+                return go(std::false_type{});
               });
             });
           }
@@ -2021,12 +2081,15 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
   const int V = pick_vec(channels, es, cell == 2 ? 8 : SIHC_RW_VEC_K4, ptrs, events + 2);
   const int S = cell * cell;
   const int E4 = (events + 3) & ~3;
+  // 16 slots, bf16 weights, 2-channel lanes: weights packed as bf16 in LDS (as sihc_read)
+  const bool wb = SIHC_K4_BF16W && cell == 4 && w_dtype == SIHC_DTYPE_BF16 && V == 2;
+  const int wbytes = wb ? 2 : 4;
   const Shape2D sh = cell == 2 ? shape_for(channels, V, SIHC_RW_BCG, E4 * S * 4)
-                               : shape_for(channels, V, SIHC_RW_BCG_K4, E4 * S * 4, SIHC_RW_LDS_K4);
+                               : shape_for(channels, V, SIHC_RW_BCG_K4, E4 * S * wbytes, SIHC_RW_LDS_K4);
   const int tpb = sh.tl * rw_tokens_per_lane(cell, E4);
   const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
   const int gs = tpb;  // one contiguous run per block (interleaved groups measured no faster)
-  const size_t lds = size_t(E4) * S * sh.bcg * V * 4;
+  const size_t lds = size_t(E4) * S * sh.bcg * V * wbytes;
   const PtrPack pk = pack(updates, events);
   auto launch = [&](auto tx, auto tw) {
     using TX = decltype(tx);
@@ -2049,12 +2112,18 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
                 constexpr int BB = decltype(bb)::value;
                 return with_hints<SIHC_WR_NTM>(hints, [&](auto nt) {
                   constexpr int NT = decltype(nt)::value;
-                  hipLaunchKernelGGL((k_write<TX, TW, VV, KK, AX, BB, NT>), dim3(blocks1d(sh.slices, chunks)),
-                                     dim3(sh.bcg, sh.tl), lds, st, static_cast<const TX*>(x), pk,
-                                     static_cast<const TW*>(beta), static_cast<TX*>(out), index, events, g, gs,
-                                     int(chunks),
-                                     sh.slices);
-                  return check_launch(what);
+                  auto go = [&](auto w) {
+                    constexpr bool WB = decltype(w)::value;
+                    hipLaunchKernelGGL((k_write<TX, TW, VV, KK, AX, BB, NT, WB>), dim3(blocks1d(sh.slices, chunks)),
+                                       dim3(sh.bcg, sh.tl), lds, st, static_cast<const TX*>(x), pk,
+                                       static_cast<const TW*>(beta), static_cast<TX*>(out), index, events, g, gs,
+                                       int(chunks), sh.slices);
+                    return check_launch(what);
+                  };
+                  if constexpr (KK == 4 && VV == 2 && std::is_same_v<TW, bf16_t>) {
+                    if (wb) return go(std::true_type{});
+                  }
+                  return go(std::false_type{});
                 });
               });
             });
