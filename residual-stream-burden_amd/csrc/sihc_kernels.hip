@@ -119,6 +119,9 @@
 #ifndef SIHC_K4_BF16W  // 1: 16-slot read / write stage bf16 weights packed as bf16 in LDS
 #define SIHC_K4_BF16W 1
 #endif
+#ifndef SIHC_K2_BF16W  // the same for 4-slot read / write (8-channel lanes)
+#define SIHC_K2_BF16W 1
+#endif
 #ifndef SIHC_RW_LDS_K4  // LDS bytes per block for staged weights, 16 slots
 #define SIHC_RW_LDS_K4 (48 * 1024)
 #endif
@@ -412,23 +415,28 @@ __device__ __forceinline__ void stage_weights(float* lds, const TW* __restrict__
   __syncthreads();
 }
 
-// bf16 weights with 2-channel lanes (16-slot read / write): the same slice as
-// stage_weights in half the LDS, one 32-bit word per (row, lane) holding the lane's two
-// channels as bf16 (low half: the even channel). Exact: a bf16 weight widens to the same
-// fp32 value either way.
-__device__ __forceinline__ void stage_weights_bf16x2(uint32_t* lds, const bf16_t* __restrict__ w, int E, int Epad,
-                                                     int S, int BCG, int cs, int C) {
+// bf16 weights (V = 2 or 8 channels per lane): the same slice as stage_weights in half
+// the LDS, V/2 32-bit words per (row, lane) holding the lane's channels as bf16 pairs
+// (low half: the even channel), so a lane reads its row with one 4- or 16-byte access and
+// consecutive lanes read consecutive words. Exact: a bf16 weight widens to the same fp32
+// value either way.
+template <int V>
+__device__ __forceinline__ void stage_weights_bf16(uint32_t* lds, const bf16_t* __restrict__ w, int E, int Epad,
+                                                   int S, int BCG, int cs, int C) {
+  constexpr int NW = V / 2;  // words per (row, lane)
   const int tid = threadIdx.y * blockDim.x + threadIdx.x;
   const int nthr = blockDim.x * blockDim.y;
-  for (int i = tid; i < Epad * BCG * S; i += nthr) {  // [e][lane][s]
-    const int e = i / (BCG * S);
-    const int r = i - e * BCG * S;
-    const int cg = r / S;
-    const int s = r - cg * S;
-    const int c = cs + 2 * cg;
+  const int BP = BCG * NW;  // channel pairs per block
+  for (int i = tid; i < Epad * BP * S; i += nthr) {  // [e][pair][s]
+    const int e = i / (BP * S);
+    const int r = i - e * BP * S;
+    const int pr = r / S;
+    const int s = r - pr * S;
+    const int c = cs + 2 * pr;
     const uint32_t lo = (e < E && c < C) ? uint32_t(w[(int64_t(e) * C + c) * S + s]) : 0u;
     const uint32_t hi = (e < E && c + 1 < C) ? uint32_t(w[(int64_t(e) * C + c + 1) * S + s]) : 0u;
-    lds[(e * S + s) * BCG + cg] = lo | (hi << 16);
+    const int cg = pr / NW, q = pr - cg * NW;
+    lds[((e * S + s) * BCG + cg) * NW + q] = lo | (hi << 16);
   }
   __syncthreads();
 }
@@ -436,10 +444,16 @@ __device__ __forceinline__ void stage_weights_bf16x2(uint32_t* lds, const bf16_t
 template <int V, bool WB>
 __device__ __forceinline__ void lds_weights(const float* lds, int row, int cg, int BCG, float (&a)[V]) {
   if constexpr (WB) {
-    static_assert(V == 2, "packed bf16 weights hold 2 channels per lane");
-    const uint32_t w = reinterpret_cast<const uint32_t*>(lds)[row * BCG + cg];
-    a[0] = __uint_as_float(w << 16);
-    a[1] = __uint_as_float(w & 0xffff0000u);
+    static_assert(V == 2 || V == 8, "packed bf16 weights: 2 or 8 channels per lane");
+    using W = typename RawT<2 * V>::type;
+    const W w = reinterpret_cast<const W*>(lds)[row * BCG + cg];
+    uint32_t u[V / 2];
+    __builtin_memcpy(u, &w, 2 * V);
+#pragma unroll
+    for (int q = 0; q < V / 2; ++q) {
+      a[2 * q] = __uint_as_float(u[q] << 16);
+      a[2 * q + 1] = __uint_as_float(u[q] & 0xffff0000u);
+    }
   } else {
 #pragma unroll
     for (int v = 0; v < V; ++v) a[v] = lds[lds_w<V>(row, cg, v, BCG)];
@@ -466,8 +480,8 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict_
   const int blk = logical_block<true>(), slice = blk % nslices, chunk = blk / nslices;
   const int cs = slice * BC;
   if constexpr (WB) {
-    stage_weights_bf16x2(reinterpret_cast<uint32_t*>(lds), reinterpret_cast<const bf16_t*>(alpha), E, E, S, BCG, cs,
-                         g.C);
+    stage_weights_bf16<V>(reinterpret_cast<uint32_t*>(lds), reinterpret_cast<const bf16_t*>(alpha), E, E, S, BCG,
+                          cs, g.C);
   } else {
     stage_weights<V>(lds, alpha, E, E, S, BCG, cs, g.C);
   }
@@ -538,8 +552,8 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restric
   const int cs = slice * BC;
   const int E4 = (E + 3) & ~3;
   if constexpr (WB) {
-    stage_weights_bf16x2(reinterpret_cast<uint32_t*>(lds), reinterpret_cast<const bf16_t*>(beta), E, E4, S, BCG, cs,
-                         g.C);
+    stage_weights_bf16<V>(reinterpret_cast<uint32_t*>(lds), reinterpret_cast<const bf16_t*>(beta), E, E4, S, BCG,
+                          cs, g.C);
   } else {
     stage_weights<V>(lds, beta, E, E4, S, BCG, cs, g.C);
   }
@@ -2011,9 +2025,10 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
   const int S = cell * cell;
   // 16 slots, bf16 weights, 2-channel lanes: weights packed as bf16 in LDS (half the
   // bytes, so twice the channels per block within the LDS budget)
-  const bool wb = SIHC_K4_BF16W && cell == 4 && dtype == SIHC_DTYPE_BF16 && V == 2;
+  const bool wb = dtype == SIHC_DTYPE_BF16 &&
+                  ((SIHC_K4_BF16W && cell == 4 && V == 2) || (SIHC_K2_BF16W && cell == 2 && V == 8));
   const int wbytes = wb ? 2 : 4;
-  const Shape2D sh = cell == 2 ? shape_for(channels, V, SIHC_RW_BCG, events * S * 4)
+  const Shape2D sh = cell == 2 ? shape_for(channels, V, SIHC_RW_BCG, events * S * wbytes)
                                : shape_for(channels, V, SIHC_RW_BCG_K4, events * S * wbytes, SIHC_RW_LDS_K4);
   const int tpb = sh.tl * rw_tokens_per_lane(cell, events, true);
   const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
@@ -2046,7 +2061,7 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
                                      static_cast<const T*>(alpha), pk, index, events, g, gs, int(chunks), sh.slices);
                   return check_launch(what);
                 };
-                if constexpr (KK == 4 && VV == 2 && std::is_same_v<T, bf16_t>) {
+                if constexpr (((KK == 4 && VV == 2) || (KK == 2 && VV == 8)) && std::is_same_v<T, bf16_t>) {
                   if (wb) return go(std::true_type{});
                 }
                 return go(std::false_type{});
@@ -2082,9 +2097,10 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
   const int S = cell * cell;
   const int E4 = (events + 3) & ~3;
   // 16 slots, bf16 weights, 2-channel lanes: weights packed as bf16 in LDS (as sihc_read)
-  const bool wb = SIHC_K4_BF16W && cell == 4 && w_dtype == SIHC_DTYPE_BF16 && V == 2;
+  const bool wb = w_dtype == SIHC_DTYPE_BF16 &&
+                  ((SIHC_K4_BF16W && cell == 4 && V == 2) || (SIHC_K2_BF16W && cell == 2 && V == 8));
   const int wbytes = wb ? 2 : 4;
-  const Shape2D sh = cell == 2 ? shape_for(channels, V, SIHC_RW_BCG, E4 * S * 4)
+  const Shape2D sh = cell == 2 ? shape_for(channels, V, SIHC_RW_BCG, E4 * S * wbytes)
                                : shape_for(channels, V, SIHC_RW_BCG_K4, E4 * S * wbytes, SIHC_RW_LDS_K4);
   const int tpb = sh.tl * rw_tokens_per_lane(cell, E4);
   const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
@@ -2120,7 +2136,7 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
                                        int(chunks), sh.slices);
                     return check_launch(what);
                   };
-                  if constexpr (KK == 4 && VV == 2 && std::is_same_v<TW, bf16_t>) {
+                  if constexpr (((KK == 4 && VV == 2) || (KK == 2 && VV == 8)) && std::is_same_v<TW, bf16_t>) {
                     if (wb) return go(std::true_type{});
                   }
                   return go(std::false_type{});
