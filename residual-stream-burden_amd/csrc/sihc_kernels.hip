@@ -135,7 +135,7 @@
 #define SIHC_TRIB_CHUNK 64
 #endif
 #ifndef SIHC_WG_TT  // most tokens per staged LDS tile of the weight / gamma gradients
-#define SIHC_WG_TT 32
+#define SIHC_WG_TT 64
 #endif
 #ifndef SIHC_WG_BCG  // most channel-group lanes per weight-gradient block
 #define SIHC_WG_BCG 64
@@ -1870,8 +1870,9 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
   const int tpb = int((int64_t(g.M) + chunks - 1) / chunks);
   // x tile of TT tokens: at most 32 KB of LDS. With 16 or fewer event lanes on the
   // carrier, 8-token tiles keep one round of update loads per tile (measured: E=16
-  // 828 -> 766 us at the XL shape; more events or the workspace mode prefer 32). The
-  // tile size does not change the summation order.
+  // 828 -> 766 us at the XL shape; more events or the workspace mode prefer up to 64:
+  // fused triangular backward A = 11 682 -> 667 us against 32). The tile size does not
+  // change the summation order.
   int tt = 32768 / (S * bcg * V * int(sizeof(float)));
   tt = std::max(1, std::min(tt, carrier && events <= 16 ? 8 : SIHC_WG_TT));
   const size_t lds = size_t(tt) * S * bcg * V * sizeof(float);
