@@ -39,7 +39,7 @@ extern "C" {
 #endif
 
 #define SIHC_MAX_EVENTS 32
-#define SIHC_ABI_VERSION 1
+#define SIHC_ABI_VERSION 2
 
 enum { SIHC_DTYPE_F32 = 0, SIHC_DTYPE_BF16 = 1 };
 enum { SIHC_OK = 0, SIHC_ERR_INVALID = 1, SIHC_ERR_HIP = 2 };
@@ -135,7 +135,8 @@ size_t sihc_event_backward_workspace_size(int64_t batch, int grid, int cell, int
  *     (the caller aliases it, as the reference's write backward does);
  *   - write part absent (beta, dz, grad_dz, grad_beta all NULL): the adjoint of a plain
  *     read, grad_x = grad_x_out + alpha (x) grad_z_out, grad_alpha = sum x * grad_z_out.
- * Weight gradients are stored in w_dtype.
+ * beta, alpha_next and the weight gradients are all in w_dtype, which must equal dtype
+ * (SIHC_ERR_INVALID otherwise).
  * Follows the adjoint formulas of sihc/docs/kernel_fusion/README.md:73-84 applied to one
  * event (the reference's autograd rules sublayer_kernels.py:280-306 with E = 1). */
 int sihc_event_backward(const void *grad_x_out, const void *grad_z_out, const void *x_out,
@@ -155,6 +156,15 @@ int sihc_gather_cells(const void *x, const int32_t *index, void *cells, int64_t 
  * cells[b,n,s]. With index == NULL it is `_cells_to_high`, reference.py:37-51. */
 int sihc_scatter_cells(const void *cells, const int32_t *index, void *x, int64_t batch,
                        int grid, int cell, int channels, int dtype, void *stream);
+
+/* Adjoint of sihc_gather_cells for any index with values in [0, grid*grid), repeats
+ * allowed: x[pixel of (n, s)] = sum over the tokens t of batch b with index[b,t] == n, in
+ * ascending t, of cells[b,t,s] (fp32 sum rounded once); cells no token selects are zero.
+ * Atomics-free and deterministic; for a permutation index it equals sihc_scatter_cells
+ * bit for bit. Out-of-range index values select no cell. index == NULL: the identity.
+ * No reference counterpart (the backward of the spatially indexed gather). */
+int sihc_scatter_add_cells(const void *cells, const int32_t *index, void *x, int64_t batch,
+                           int grid, int cell, int channels, int dtype, void *stream);
 
 /* Plain device copy of `bytes` bytes (16-byte vectors). No reference counterpart: it is
  * the calibration kernel for HBM counters and the practical bandwidth ceiling. */

@@ -231,6 +231,26 @@ def scatter_cells(cells: Tensor, index: Optional[Tensor]) -> Tensor:
     return cells_to_high(out)
 
 
+def scatter_add_cells(cells: Tensor, index: Tensor) -> Tensor:
+    """Adjoint of gather_cells for any in-range index (repeats allowed): state n of batch
+    b receives the fp32 sum, over the tokens t with index[b,t] == n in ascending t, of
+    cells[b,t], rounded once to the cells' dtype; states no token selects are zero. The
+    sum starts from -0.0 (the identity of fp32 addition: one contributor is copied bit
+    for bit). Builder-defined semantics (the reference has no indexed variant); pinned
+    by torch's index_add_ on exactly representable sums and by the permutation case,
+    where it must equal scatter_cells."""
+    b_n, n_tok, s_n, c = cells.shape
+    acc = torch.full((b_n, n_tok, s_n, c), -0.0, dtype=torch.float32)
+    hits = torch.zeros(b_n, n_tok, dtype=torch.int64)
+    rows = torch.arange(b_n)
+    idx = index.long()
+    for t in range(n_tok):  # one index per batch row per step: no conflicts within a step
+        acc[rows, idx[:, t]] += cells[:, t].float()
+        hits[rows, idx[:, t]] += 1
+    acc[hits == 0] = 0.0
+    return cells_to_high(acc.to(cells.dtype))
+
+
 # --------------------------------------------------------------------------------
 # (2) float64 brute force (explicit loops; small shapes only)
 # --------------------------------------------------------------------------------

@@ -1484,6 +1484,50 @@ __global__ void __launch_bounds__(256) k_cells(const R* __restrict__ src, R* __r
   }
 }
 
+// ----------------------------------------------------------------------------------
+// adjoint of the gather for any in-range index (repeats allowed): the cell n of batch b
+// receives the fp32 sum, over the tokens t of row b with index[b,t] == n in ascending t,
+// of cells[b,t]; cells that no token selects receive zeros. One block per destination
+// cell: the batch row of the index is staged in LDS and every thread scans it in order
+// (a block-uniform test, so no divergence). No atomics: deterministic. The sum starts
+// from -0.0 (the identity of fp32 addition), so a cell with one contributor receives its
+// value bit for bit, as the scatter copy would.
+// ----------------------------------------------------------------------------------
+template <typename T, int V, int K>
+__global__ void __launch_bounds__(256) k_cells_add(const T* __restrict__ cells, T* __restrict__ x,
+                                                   const int32_t* __restrict__ index, Geo g) {
+  constexpr int S = K * K;
+  extern __shared__ int32_t sidx[];
+  const int64_t m = blockIdx.x;  // destination cell b * GG + n
+  const int b = int(m / g.GG), n = int(m - int64_t(b) * g.GG);
+  for (int t = threadIdx.x; t < g.GG; t += blockDim.x) sidx[t] = index[int64_t(b) * g.GG + t];
+  __syncthreads();
+  const int64_t pix0 = cell_pixel0(int(m), g, nullptr);
+  const int nvec = S * g.C / V;
+  for (int i = threadIdx.x; i < nvec; i += blockDim.x) {
+    const int e = i * V;
+    const int s = e / g.C;
+    const int c = e - s * g.C;
+    float acc[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[v] = -0.f;
+    int hits = 0;
+    for (int t = 0; t < g.GG; ++t) {
+      if (sidx[t] != n) continue;
+      float val[V];
+      load_vec<T, V>(cells + ((int64_t(b) * g.GG + t) * S + s) * g.C + c, val);
+#pragma unroll
+      for (int v = 0; v < V; ++v) acc[v] += val[v];
+      ++hits;
+    }
+    if (hits == 0) {
+#pragma unroll
+      for (int v = 0; v < V; ++v) acc[v] = 0.f;
+    }
+    store_vec<T, V>(x + slot_offset<K>(pix0, s, g, c), acc);
+  }
+}
+
 __global__ void __launch_bounds__(256) k_copy16(const u32x4* __restrict__ src, u32x4* __restrict__ dst, int64_t n) {
   const int64_t stride = int64_t(gridDim.x) * blockDim.x;
   constexpr bool NTL = (SIHC_COPY_NTM & 1) != 0, NTS = (SIHC_COPY_NTM & 2) != 0;
@@ -1842,6 +1886,38 @@ int cells_copy(const char* what, bool gather, const void* src, const int32_t* in
   if (row_bytes % 16 == 0 && aligned(src, 16) && aligned(dst, 16)) return go(u32x4{});
   if (row_bytes % 4 == 0 && aligned(src, 4) && aligned(dst, 4)) return go(uint32_t{});
   return go(uint16_t{});
+}
+
+// Adjoint of the gather (k_cells_add): one block per destination cell.
+int cells_add(const char* what, const void* cells, const int32_t* index, void* x, int64_t batch, int grid, int cell,
+              int channels, int dtype, void* stream) {
+  Geo g;
+  if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
+  if (!valid_dtype(dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype %d", what, dtype);
+  if (g.M == 0) return SIHC_OK;  // empty tensors may carry NULL data pointers
+  if (!cells || !x) return fail(SIHC_ERR_INVALID, "%s: null pointer", what);
+  if (!index) return cells_copy(what, false, cells, nullptr, x, batch, grid, cell, channels, dtype, stream);
+  if (g.GG > 16384) return fail(SIHC_ERR_INVALID, "%s: grid of %d cells exceeds 16384", what, g.GG);
+  const void* ptrs[] = {cells, x};
+  const int V = pick_vec(channels, elem_size(dtype), 8, ptrs, 2);
+  const size_t lds = size_t(g.GG) * sizeof(int32_t);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return with_dtype(dtype, [&](auto t) {
+    using T = decltype(t);
+    return with_vec(V, [&](auto vv) {
+      constexpr int VV = decltype(vv)::value;
+      if constexpr (VV * sizeof(T) > 16) {
+        return fail(SIHC_ERR_INVALID, "%s: internal vector width", what);
+      } else {
+        return with_cell(cell, [&](auto kk) {
+          constexpr int KK = decltype(kk)::value;
+          hipLaunchKernelGGL((k_cells_add<T, VV, KK>), dim3(unsigned(g.M)), dim3(256), lds, st,
+                             static_cast<const T*>(cells), static_cast<T*>(x), index, g);
+          return check_launch(what);
+        });
+      }
+    });
+  });
 }
 
 // Shared launcher of the atomics-free weight-gradient reduction + finalize. With
@@ -2334,15 +2410,19 @@ size_t sihc_event_backward_workspace_size(int64_t batch, int grid, int cell, int
   return size_t(event_bwd_chunks(M)) * 2 * cell * cell * channels * sizeof(float);
 }
 
-int sihc_event_backward(const void* grad_x_out, const void* grad_z_out, const void* x_out, const void* dz,
-                        const void* beta, const void* alpha_next, void* grad_x, void* grad_dz, void* grad_beta,
-                        void* grad_alpha_next, int64_t batch, int grid, int cell, int channels,
-                        const int32_t* index, int dtype, int w_dtype, void* workspace, size_t workspace_bytes,
-                        void* stream) {
-  const char* what = "sihc_event_backward";
+// implementation of sihc_event_backward (errors name the entry point)
+static int event_backward_impl(const char* what, const void* grad_x_out, const void* grad_z_out, const void* x_out,
+                               const void* dz, const void* beta, const void* alpha_next, void* grad_x, void* grad_dz,
+                               void* grad_beta, void* grad_alpha_next, int64_t batch, int grid, int cell,
+                               int channels, const int32_t* index, int dtype, int w_dtype, void* workspace,
+                               size_t workspace_bytes, void* stream) {
   Geo g;
   if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
   if (!valid_dtype(dtype) || !valid_dtype(w_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
+  // beta / alpha_next are read as `dtype`, and their gradients share their dtype
+  if (w_dtype != dtype)
+    return fail(SIHC_ERR_INVALID, "%s: weights must share the carrier dtype (w_dtype %d, dtype %d)", what, w_dtype,
+                dtype);
   const int S = cell * cell;
   const int64_t wn = int64_t(S) * channels;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -2423,9 +2503,20 @@ int sihc_event_backward(const void* grad_x_out, const void* grad_z_out, const vo
   });
   if (rc) return rc;
   // Partial rows are [chunks][2][S][C]: row 0 -> grad_beta, row 1 -> grad_alpha_next
-  // (written as zeros when there is no read part).
+  // (written as zeros when there is no read part). A part the kernel did not run has no
+  // partial rows, so the finalize does not read them.
   return launch_finalize(what, part, has_w ? grad_beta : nullptr, grad_alpha_next, chunks, 2, S, channels, true,
-                         has_g ? 0 : 2, w_dtype, st);
+                         (has_w ? 0 : 1) | (has_g ? 0 : 2), w_dtype, st);
+}
+
+int sihc_event_backward(const void* grad_x_out, const void* grad_z_out, const void* x_out, const void* dz,
+                        const void* beta, const void* alpha_next, void* grad_x, void* grad_dz, void* grad_beta,
+                        void* grad_alpha_next, int64_t batch, int grid, int cell, int channels,
+                        const int32_t* index, int dtype, int w_dtype, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  return event_backward_impl("sihc_event_backward", grad_x_out, grad_z_out, x_out, dz, beta, alpha_next, grad_x,
+                             grad_dz, grad_beta, grad_alpha_next, batch, grid, cell, channels, index, dtype, w_dtype,
+                             workspace, workspace_bytes, stream);
 }
 
 int sihc_gather_cells(const void* x, const int32_t* index, void* cells, int64_t batch, int grid, int cell,
@@ -2436,6 +2527,11 @@ int sihc_gather_cells(const void* x, const int32_t* index, void* cells, int64_t 
 int sihc_scatter_cells(const void* cells, const int32_t* index, void* x, int64_t batch, int grid, int cell,
                        int channels, int dtype, void* stream) {
   return cells_copy("sihc_scatter_cells", false, cells, index, x, batch, grid, cell, channels, dtype, stream);
+}
+
+int sihc_scatter_add_cells(const void* cells, const int32_t* index, void* x, int64_t batch, int grid, int cell,
+                           int channels, int dtype, void* stream) {
+  return cells_add("sihc_scatter_add_cells", cells, index, x, batch, grid, cell, channels, dtype, stream);
 }
 
 int sihc_copy(const void* src, void* dst, size_t bytes, void* stream) {

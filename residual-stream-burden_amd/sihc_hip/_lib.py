@@ -10,7 +10,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libsihc_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 MAX_EVENTS = 32
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -40,6 +40,7 @@ PROTOTYPES: dict[str, tuple] = {
                                    _i64, _i32, _i32, _i32, _vp, _i32, _i32, _vp, _sz, _vp]),
     "sihc_gather_cells": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
     "sihc_scatter_cells": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
+    "sihc_scatter_add_cells": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
     "sihc_copy": (_i32, [_vp, _vp, _sz, _vp]),
 }
 

@@ -5,7 +5,11 @@ Specification (the reference has no such op; this module defines it):
 * ``index`` is an int32 tensor [B, G*G]. Token (b, n) of the workspace is assigned
   the prediction state (carrier cell) ``index[b, n]`` of batch b: the K*K carrier
   pixels (b, wy*K+uy, wx*K+ux) with wy, wx = divmod(index[b, n], G).
-* gather:  cells[b, n, s, :] = x[pixel (index[b, n], s), :]   -- bit-exact copies
+* gather:  cells[b, n, s, :] = x[pixel (index[b, n], s), :]   -- bit-exact copies; any
+  index with values in [0, G*G) (repeats allowed). Its adjoint is a scatter-add: each
+  state receives the fp32 sum, in ascending token order, of the gradient rows of the
+  tokens that selected it (zero where none did), rounded once -- atomics-free and
+  deterministic, and bit-identical to the scatter for a permutation index.
 * scatter: x[pixel (index[b, n], s), :] = cells[b, n, s, :]   -- index must be a
   permutation of 0..G*G-1 in every batch row (each state written exactly once)
 * indexed read/write: the read/write maps applied to the gathered states, and the
@@ -166,13 +170,25 @@ def _scatter_cells_fake(cells, index):
     return cells.new_empty((b, g * k, g * k, c))
 
 
+@custom_op("sihc::scatter_add_cells", mutates_args=())
+def _scatter_add_cells(cells: Tensor, index: Tensor) -> Tensor:
+    return launch.scatter_add_cells(cells, index)
+
+
+@_scatter_add_cells.register_fake
+def _scatter_add_cells_fake(cells, index):
+    return _scatter_cells_fake(cells, index)
+
+
 def _gather_setup(ctx, inputs, output):
     ctx.save_for_backward(inputs[1])
 
 
 def _gather_backward(ctx, grad):
+    # the gather accepts repeated indices: its adjoint sums the rows of every token
+    # that selected a state (and leaves unselected states at zero)
     (index,) = ctx.saved_tensors
-    return _scatter_cells(grad.contiguous(), index), None, None
+    return _scatter_add_cells(grad.contiguous(), index), None, None
 
 
 def _scatter_setup(ctx, inputs, output):

@@ -189,6 +189,9 @@ def event_backward(grad_x_out: Optional[Tensor], grad_z_out: Optional[Tensor], x
     """
     ref = x_out if x_out is not None else (carrier_like if carrier_like is not None else grad_x_out)
     w = beta if beta is not None else alpha_next
+    for t in (beta, alpha_next):
+        if t is not None and t.dtype != ref.dtype:
+            raise ValueError(f"event weights must share the carrier dtype {ref.dtype}, got {t.dtype}")
     b, g, k, c = carrier_geometry(ref, w.shape[1])
     alias = alias_grad_x and grad_z_out is None
     if alias:
@@ -232,6 +235,21 @@ def scatter_cells(cells: Tensor, index: Optional[Tensor], out: Optional[Tensor] 
 
 
 @_on_tensor_device
+def scatter_add_cells(cells: Tensor, index: Optional[Tensor], out: Optional[Tensor] = None) -> Tensor:
+    """Adjoint of gather_cells for any in-range index (repeats allowed): each carrier cell
+    gets the fp32 sum, in ascending token order, of the cells rows that select it, and
+    zeros where none does. Equals scatter_cells bit for bit for a permutation index."""
+    b, n, s, c = cells.shape
+    k = 2 if s == 4 else 4
+    g = int(round(n ** 0.5))
+    if out is None:
+        out = torch.empty((b, g * k, g * k, c), device=cells.device, dtype=cells.dtype)
+    check(lib().sihc_scatter_add_cells(cells.data_ptr(), _ptr(index), out.data_ptr(), b, g, k, c,
+                                       dtype_code(cells.dtype), _stream(cells.device)))
+    return out
+
+
+@_on_tensor_device
 def copy_(dst: Tensor, src: Tensor) -> Tensor:
     """Byte copy src -> dst (same number of bytes) with the library's copy kernel."""
     nbytes = src.numel() * src.element_size()
@@ -244,5 +262,5 @@ def copy_(dst: Tensor, src: Tensor) -> Tensor:
 __all__ = [
     "MAX_EVENTS", "dtype_code", "carrier_geometry", "read", "write", "weight_grad", "triangular",
     "triangular_gamma_grad", "triangular_backward", "event_forward", "event_backward", "gather_cells",
-    "scatter_cells", "copy_",
+    "scatter_cells", "scatter_add_cells", "copy_",
 ]

@@ -193,49 +193,49 @@ def _tri_autograd(ctx, grad):
 register_autograd(sublayer_triangular, _tri_autograd, setup_context=_tri_setup)
 
 
-# Fake implementations (reference :387-416): shape-only, device-free, for fullgraph
-# torch.compile and HIP-graph capture through the compiler.
+# Fake implementations (reference :387-416): device-free shape functions for fullgraph
+# torch.compile and HIP-graph capture through the compiler. They run the same layout,
+# geometry and update checks as the real ops (the reference's read and write fakes call
+# `_geometry` / `_validate_updates`, :387-398; here the weight-gradient and triangular
+# fakes check their operands too), so a bad shape fails at trace time, not at launch.
 @sublayer_read.register_fake
 def _read_fake(x, alpha):
-    b, c, g, _ = _geometry_fake(x, alpha)
+    b, c, g, _ = _geometry(x, alpha)
     return [x.new_empty((b, g * g, c)) for _ in range(alpha.shape[0])]
-
-
-def _geometry_fake(x, weights):
-    if x.ndim != 4 or weights.ndim != 3:
-        raise ValueError("expected NHWC carrier and [events, channels, slots] weights")
-    b, h, _, c = x.shape
-    k = 2 if weights.shape[2] == 4 else 4
-    return b, c, h // k, k
 
 
 @_write_impl.register_fake
 def _write_impl_fake(x, updates, beta, add_x):
+    _validate_updates(x, beta, updates)
     return torch.empty_like(x)
 
 
 @sublayer_write.register_fake
 def _write_fake(x, updates, beta):
-    return torch.empty_like(x)
+    return _write_impl_fake(x, updates, beta, True)
 
 
 @_weights_backward.register_fake
 def _weight_fake(x, updates, weights):
-    return weights.new_empty((len(updates), weights.shape[1], weights.shape[2]))
+    _validate_updates(x, weights, updates)
+    return torch.empty_like(weights)
 
 
 @sublayer_triangular.register_fake
 def _tri_fake(base, updates, gamma):
+    _validate_triangular(base, updates, gamma)
     return torch.empty_like(base)
 
 
 @_tri_gamma_backward.register_fake
 def _tri_gamma_backward_fake(grad, updates, gamma):
+    _validate_triangular(grad, updates, gamma)
     return torch.empty_like(gamma)
 
 
 @_tri_backward.register_fake
 def _tri_backward_fake(grad, updates, gamma):
+    _validate_triangular(grad, updates, gamma)
     return grad.new_empty((len(updates), *grad.shape)), torch.empty_like(gamma)
 
 

@@ -33,3 +33,26 @@ def _no_tf32():
     torch.backends.cuda.matmul.allow_tf32 = False
     torch.backends.cudnn.allow_tf32 = False
     yield
+
+
+def pytest_terminal_summary(terminalreporter):
+    """Worst achieved parity margins per bar (the achieved errors of every check)."""
+    from helpers import RECORDS
+
+    if not RECORDS:
+        return
+    tr = terminalreporter
+    tr.section("parity margins")
+    for kind in ("elementwise", "reduced", "chained", "fp32"):
+        rows = [r for r in RECORDS if r[3] == kind]
+        if not rows:
+            continue
+        worst_rel = max(rows, key=lambda r: r[7])
+        line = f"{kind:11s} {len(rows):4d} checks; worst rel-L2 {worst_rel[7]:.2e} ({worst_rel[1]}, {worst_rel[0]})"
+        if kind == "elementwise":
+            worst = max(rows, key=lambda r: r[6])
+            line += f"; worst {worst[6]:.2f} ulp ({worst[1]}, {worst[0]})"
+        else:
+            worst = max(rows, key=lambda r: r[4] / max(r[5], 1e-30))
+            line += f"; worst max-abs/scale {worst[4] / max(worst[5], 1e-30):.2e} ({worst[1]}, {worst[0]})"
+        tr.write_line(line)

@@ -101,6 +101,27 @@ def test_triangular_backward_arguments_are_validated():
     assert b"1..32" in lib.sihc_last_error()
 
 
+def test_event_backward_weight_dtype_must_match_carrier():
+    # beta / alpha_next are read as the carrier dtype: fp32 weights with a bf16 carrier
+    # would be reinterpreted, so the mismatch is an argument error
+    lib = _lib.lib()
+    rc = lib.sihc_event_backward(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                 2, 16, 2, 64, None, _lib.DTYPE_BF16, _lib.DTYPE_F32, FAKE, 1 << 30, None)
+    assert rc == 1 and b"weights must share the carrier dtype" in lib.sihc_last_error()
+
+
+def test_scatter_add_cells_arguments_are_validated():
+    lib = _lib.lib()
+    assert lib.sihc_scatter_add_cells(FAKE, FAKE, None, 2, 16, 2, 64, _lib.DTYPE_BF16, None) == 1
+    assert b"null pointer" in lib.sihc_last_error()
+    assert lib.sihc_scatter_add_cells(FAKE, FAKE, FAKE, 2, 16, 2, 64, 9, None) == 1
+    assert b"bad dtype" in lib.sihc_last_error()
+    assert lib.sihc_scatter_add_cells(FAKE, FAKE, FAKE, 2, 16, 3, 64, _lib.DTYPE_BF16, None) == 1
+    assert b"cell must be 2 or 4" in lib.sihc_last_error()
+    # empty batch: nothing to do, no pointer is touched
+    assert lib.sihc_scatter_add_cells(None, None, None, 0, 16, 2, 64, _lib.DTYPE_BF16, None) == 0
+
+
 def test_oversized_tensor_is_rejected():
     lib = _lib.lib()
     outs = _lib.ptr_array([FAKE])

@@ -54,8 +54,9 @@ def test_fullgraph_compile_of_stage_forward_backward(dtype):
     out = compiled(*leaves2)
     gc = torch.autograd.grad(out, leaves2, go)
     assert torch.equal(out, eager)
+    # the traced backward may add the autograd contributions in another order
     for a, b in zip(gc, ge):
-        assert_parity(a, b, dtype)
+        assert_parity(a, b, dtype, kind="chained")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -77,7 +78,7 @@ def test_fullgraph_compile_of_literal_stage(dtype):
     gc = torch.autograd.grad(out, leaves2, go)
     assert torch.equal(out, eager)
     for a, b in zip(gc, ge):
-        assert_parity(a, b, dtype)
+        assert_parity(a, b, dtype, kind="chained")
 
 
 def test_hip_graph_capture_and_replay_of_stage_forward():

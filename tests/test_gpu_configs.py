@@ -59,8 +59,8 @@ def test_config2_event_forward_and_backward_full_batch():
         t = O.high_to_cells(hc[b0:b0 + 16], 4).double() + gzc[b0:b0 + 16].double().unsqueeze(2) * a64.T[None, None]
         db += torch.einsum("bnsc,bnc->cs", t, dzc[b0:b0 + 16].double())
         da += torch.einsum("bnsc,bnc->cs", O.high_to_cells(xoc[b0:b0 + 16], 4).double(), gzc[b0:b0 + 16].double())
-    assert_parity(gb, db, BF16, what="grad_beta (65,536 tokens)")
-    assert_parity(ga, da, BF16, what="grad_alpha (65,536 tokens)")
+    assert_parity(gb, db, BF16, what="grad_beta (65,536 tokens)", kind="reduced")
+    assert_parity(ga, da, BF16, what="grad_alpha (65,536 tokens)", kind="reduced")
 
 
 def test_config1_stage_read_write_24_events():
@@ -87,7 +87,7 @@ def test_config1_stage_read_write_24_events():
             cells = O.high_to_cells(x[b0:b0 + 32, :, :, cs].cpu(), 4).double()
             z = torch.stack([u[b0:b0 + 32, :, cs].cpu().double() for u in ups])
             exp += torch.einsum("bnsc,ebnc->ecs", cells, z)
-        assert_parity(wg[:, cs], exp, BF16, what=f"weight grad channels {cs}")
+        assert_parity(wg[:, cs], exp, BF16, what=f"weight grad channels {cs}", kind="reduced")
 
 
 def test_config3_indexed_gather_scatter_full_size():
@@ -97,6 +97,47 @@ def test_config3_indexed_gather_scatter_full_size():
     cells = gather_cells(x, idx, validate=True)
     assert torch.equal(cells.cpu(), O.gather_cells(x.cpu(), idx.cpu(), 4))
     assert torch.equal(scatter_cells(cells, idx), x)
+
+
+def test_config3_indexed_event_forward_and_backward_full_size():
+    # The timed config-3 workload: batch 128, D = 1152, the seeded group-of-5 state index.
+    # Per-token outputs on batch slices against gather -> oracle -> scatter; the weight
+    # gradients over all 32,768 tokens against float64 sums of the gathered states.
+    announce("config3 shape B128 D1152 bf16 indexed event fwd+bwd")
+    x, alpha, beta, dz = _draw(128, 1152, seed=3)
+    idx = group_index(128, 16, 5, seed=3).cuda()
+    x_out, z_out = launch.event_forward(x, dz, beta, alpha, index=idx)
+    for sl in (slice(0, 2), slice(126, 128)):
+        ic = idx[sl].cpu()
+        states = O.cells_to_high(O.gather_cells(x[sl].cpu(), ic, 4))  # token-ordered carrier
+        rx, rz = O.event_forward(states, dz[sl].cpu(), beta.cpu(), alpha.cpu())
+        assert_parity(x_out[sl], O.scatter_cells(O.high_to_cells(rx, 4), ic), BF16, what="indexed x_out slice")
+        assert_parity(z_out[sl], rz, BF16, what="indexed z_out slice")
+    g = torch.Generator(device="cuda").manual_seed(33)
+    h = (1e-2 * torch.randn(x.shape, device="cuda", generator=g)).to(BF16)
+    gz = (1e-2 * torch.randn(dz.shape, device="cuda", generator=g)).to(BF16)
+    gx, gdz, gb, ga = launch.event_backward(h, gz, x_out, dz, beta, alpha, index=idx)
+    again = launch.event_backward(h, gz, x_out, dz, beta, alpha, index=idx)
+    for a, b in zip((gx, gdz, gb, ga), again):
+        assert torch.equal(a, b)
+    for sl in (slice(0, 2), slice(126, 128)):
+        ic = idx[sl].cpu()
+        gather = lambda t: O.cells_to_high(O.gather_cells(t[sl].cpu(), ic, 4))  # noqa: E731
+        ref = O.event_backward(gather(h), gz[sl].cpu(), gather(x_out), dz[sl].cpu(), beta.cpu(), alpha.cpu())
+        assert_parity(gx[sl], O.scatter_cells(O.high_to_cells(ref[0], 4), ic), BF16, what="indexed grad_x slice")
+        assert_parity(gdz[sl], ref[1], BF16, what="indexed grad_dz slice")
+    ic = idx.cpu()
+    hc, gzc, xoc, dzc = h.cpu(), gz.cpu(), x_out.cpu(), dz.cpu()
+    db = torch.zeros(1152, 4, dtype=torch.float64)
+    da = torch.zeros(1152, 4, dtype=torch.float64)
+    a64 = alpha.cpu().double()
+    for b0 in range(0, 128, 16):
+        bs = slice(b0, b0 + 16)
+        t = O.gather_cells(hc[bs], ic[bs], 4).double() + gzc[bs].double().unsqueeze(2) * a64.T[None, None]
+        db += torch.einsum("bnsc,bnc->cs", t, dzc[bs].double())
+        da += torch.einsum("bnsc,bnc->cs", O.gather_cells(xoc[bs], ic[bs], 4).double(), gzc[bs].double())
+    assert_parity(gb, db, BF16, what="indexed grad_beta (32,768 tokens)", kind="reduced")
+    assert_parity(ga, da, BF16, what="indexed grad_alpha (32,768 tokens)", kind="reduced")
 
 
 def test_carrier_over_2_pow_31_elements():

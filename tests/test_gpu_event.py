@@ -53,9 +53,9 @@ def test_event_backward_matches_adjoint(dtype, slots, has_h, has_g):
                            dz.cpu(), beta.cpu(), alpha.cpu())
     assert_parity(gx, ref[0], dtype, what="grad_x")
     assert_parity(gdz, ref[1], dtype, what="grad_dz")
-    assert_parity(gb, ref[2], dtype, what="grad_beta")
+    assert_parity(gb, ref[2], dtype, what="grad_beta", kind="reduced")
     if has_g:
-        assert_parity(ga, ref[3], dtype, what="grad_alpha_next")
+        assert_parity(ga, ref[3], dtype, what="grad_alpha_next", kind="reduced")
     else:
         assert torch.count_nonzero(ga) == 0
     # deterministic reductions
@@ -87,7 +87,7 @@ def test_event_backward_many_interleaved_chunks(dtype, slots, batch, grid):
     ref = O.event_backward(cells(h), g.cpu(), cells(x_out), dz.cpu(), beta.cpu(), alpha.cpu())
     assert_parity(O.cells_to_high(O.gather_cells(got[0].cpu(), index, slots)), ref[0], dtype, what="grad_x")
     for name, a, b in zip(("grad_dz", "grad_beta", "grad_alpha_next"), got[1:], ref[1:]):
-        assert_parity(a, b, dtype, what=name)
+        assert_parity(a, b, dtype, what=name, kind="elementwise" if name == "grad_dz" else "reduced")
     again = launch.event_backward(h, g, x_out, dz, beta, alpha, index=index.cuda())
     for a, b in zip(got, again):
         assert torch.equal(a, b)
@@ -112,9 +112,11 @@ def test_literal_stage_forward_and_gradients(dtype, slots):
     xc, ac, bc = (t.detach().cpu().clone().requires_grad_() for t in (x, alpha, beta))
     ref = O.literal_stage(xc, ac, bc, fns)
     rgrads = torch.autograd.grad(ref, (xc, ac, bc), go.cpu())
-    assert_parity(out, ref, dtype, what="carrier")
+    # six events deep: every event's carrier is rounded on both sides, so neighbouring
+    # ulps compound
+    assert_parity(out, ref, dtype, what="carrier", kind="chained")
     for name, a, b in zip(("dX", "dalpha", "dbeta"), grads, rgrads):
-        assert_parity(a, b, dtype, what=name)
+        assert_parity(a, b, dtype, what=name, kind="chained")
 
 
 def test_event_op_handles_unused_outputs():

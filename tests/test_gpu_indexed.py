@@ -50,6 +50,34 @@ def test_gather_accepts_shared_states_and_rejects_bad_indices():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("slots,channels", [(4, 67), (4, 64), (16, 24)])
+def test_gather_backward_sums_repeated_states(dtype, slots, channels):
+    # The gather accepts repeated indices; its adjoint adds the gradient rows of every
+    # token that selected a state (fp32, ascending token order, one rounding) and leaves
+    # unselected states at zero. Same summation order as the oracle: bit for bit.
+    announce(f"gather backward repeated index dtype={dtype} slots={slots} C={channels}")
+    torch.manual_seed(12)
+    k = O.cell_edge(slots)
+    x = torch.randn(3, 16 * k, 16 * k, channels, device="cuda", dtype=dtype).requires_grad_()
+    idx = torch.randint(0, 256, (3, 256), device="cuda", dtype=torch.int32)
+    idx[:, 10:20] = 7  # one state selected at least ten times per row
+    cells = gather_cells(x, idx, slots)
+    g = torch.randn_like(cells)
+    (gx,) = torch.autograd.grad(cells, x, g)
+    want = O.scatter_add_cells(g.cpu(), idx.cpu())
+    assert torch.equal(gx.cpu(), want)
+    # cells no token selected receive exactly zero
+    unselected = torch.ones(3, 256, dtype=torch.bool)
+    unselected[torch.arange(3)[:, None], idx.cpu().long()] = False
+    assert unselected.any()
+    assert (O.high_to_cells(gx.detach().cpu(), slots)[unselected] == 0).all()
+    # a permutation index: the adjoint is the scatter copy, bit for bit
+    perm = group_index(3, 16, 5, seed=4).cuda()
+    (gp,) = torch.autograd.grad(gather_cells(x, perm, slots), x, g)
+    assert torch.equal(gp, scatter_cells(g, perm))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_identity_index_is_bit_identical_to_plain_ops(dtype):
     announce(f"identity index dtype={dtype}")
     torch.manual_seed(6)
@@ -91,5 +119,8 @@ def test_indexed_read_write_match_gather_apply_scatter(dtype):
     for e in range(events):
         assert_parity(z[e], zr[e], dtype, what=f"z[{e}]")
     assert_parity(xo, xr, dtype, what="carrier")
+    # grads: x (two events' adjoints added by autograd in bf16 on both sides), alpha and
+    # beta (token reductions), the updates (one read each)
     for i, (g, r) in enumerate(zip(grads, rgrads)):
-        assert_parity(g, r, dtype, what=f"grad[{i}]")
+        kind = "chained" if i == 0 else ("reduced" if i in (1, 2) else "elementwise")
+        assert_parity(g, r, dtype, what=f"grad[{i}]", kind=kind)

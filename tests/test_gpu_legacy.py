@@ -63,7 +63,7 @@ def test_triangular_active_ops_forward_and_fused_backward(stage, active, dtype):
         else:
             assert_parity(a, r, dtype, what=f"grad dz{i}")
     assert grads[-1].dtype == dtype
-    assert_parity(grads[-1], rgrads[-1], dtype, what="grad gamma")
+    assert_parity(grads[-1], rgrads[-1], dtype, what="grad gamma", kind="reduced")
     assert torch.count_nonzero(grads[-1][active:]) == 0
 
 
@@ -87,7 +87,7 @@ def test_all_base_split_forward_and_backward(tag, dtype):
     ex, ea = torch.autograd.grad(ref, (rx, ra), [u.cpu().double() for u in upstream])
     assert gx.dtype == dtype and ga.dtype == dtype
     assert_parity(gx, ex, dtype, what="grad x0")
-    assert_parity(ga, ea, dtype, what="grad alpha")
+    assert_parity(ga, ea, dtype, what="grad alpha", kind="reduced")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -110,7 +110,7 @@ def test_final_accumulate_forward_and_backward(tag, dtype):
     rgrads = torch.autograd.grad(ref, leaves, upstream.cpu().double())
     for i, (a, r) in enumerate(zip(grads, rgrads)):
         assert a.dtype == dtype
-        assert_parity(a, r, dtype, what=f"grad input {i}")
+        assert_parity(a, r, dtype, what=f"grad input {i}", kind="reduced" if i > blocks else "elementwise")
 
 
 def test_final_accumulate_fp32_carrier_with_bf16_updates():
@@ -129,7 +129,8 @@ def test_final_accumulate_fp32_carrier_with_bf16_updates():
     leaves = _f64([x, *dzs, *betas])
     rgrads = torch.autograd.grad(O.write_torch(leaves[0], leaves[1:9], leaves[9:]), leaves, upstream.cpu().double())
     for i, (a, r) in enumerate(zip(grads, rgrads)):
-        assert_parity(a, r, torch.float32 if i == 0 else torch.bfloat16, what=f"grad input {i}")
+        assert_parity(a, r, torch.float32 if i == 0 else torch.bfloat16, what=f"grad input {i}",
+                      kind="reduced" if i > 8 else "elementwise")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -238,8 +239,9 @@ def test_legacy_stage_equals_sublayer_stage_and_compiles(blocks, dtype):
     comp = torch.compile(_legacy_stage, backend="aot_eager", fullgraph=True)(*comp_leaves)
     comp_grads = torch.autograd.grad(comp, comp_leaves, go)
     assert torch.equal(comp, out)
+    # the traced backward may add the autograd contributions in another order
     for a, b in zip(comp_grads, grads):
-        assert_parity(a, b, dtype)
+        assert_parity(a, b, dtype, kind="chained")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -255,7 +257,7 @@ def test_few_event_reductions_direct_and_staged(events, c, dtype):
     ups = [torch.randn(3, 49, c, device="cuda", dtype=dtype) for _ in range(events)]
     w = torch.randn(events, c, 4, device="cuda", dtype=dtype)
     assert_parity(launch.weight_grad(x, ups, w), O.weight_grad(x.cpu(), [u.cpu() for u in ups], 4).to(dtype),
-                  dtype, what="carrier weight grad")
+                  dtype, what="carrier weight grad", kind="reduced")
     grad = torch.randn(3, 49, c, device="cuda", dtype=dtype)
     gamma = torch.randn(events, c, device="cuda")
     ddz, dg = launch.triangular_backward(grad, ups, gamma)

@@ -43,8 +43,13 @@ def test_read_and_adjoint_with_token_and_channel_tails(dtype, slots, events):
     rgx, rga = torch.autograd.grad(sum((z * u.cpu()).sum() for z, u in zip(ref, up)), (xc, ac))
     for e in range(events):
         assert_parity(out[e], ref[e], dtype, what=f"z[{e}]")
-    assert_parity(gx, rgx, dtype, what="dX")
-    assert_parity(ga, rga, dtype, what="dalpha")
+    # the oracle's autograd rounds each event's contribution to dX and adds them in bf16;
+    # the kernel sums all events in fp32 and rounds once, so it is checked against the
+    # exact (float64) adjoint sum_e alpha_e * up_e at the 1-ulp bar
+    assert_parity(gx, rgx, dtype, what="dX vs oracle autograd", kind="elementwise" if events == 1 else "chained")
+    exact = O.write(xc.detach().double(), [u.cpu().double() for u in up], ac.detach().double(), add_x=False)
+    assert_parity(gx, exact, dtype, what="dX vs exact adjoint")
+    assert_parity(ga, rga, dtype, what="dalpha", kind="reduced")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -69,7 +74,7 @@ def test_write_forward_and_adjoint(dtype, slots, events):
     assert_parity(out, ref, dtype, what="X'")
     assert grads[0].data_ptr() == go.data_ptr() or torch.equal(grads[0], go)  # identity carry
     for i, (a, b) in enumerate(zip(grads, rgrads)):
-        assert_parity(a, b, dtype, what=f"grad[{i}]")
+        assert_parity(a, b, dtype, what=f"grad[{i}]", kind="reduced" if i == events + 1 else "elementwise")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -94,7 +99,10 @@ def test_triangular_forward_and_gradients(dtype, active, gamma_fp32):
     rgrads = torch.autograd.grad(rloss, (bc, *uc, gc))
     assert_parity(out, ref, dtype, what="tri")
     for i, (a, b) in enumerate(zip(grads, rgrads)):
-        assert_parity(a, b, dtype if i < active + 1 else gdt, what=f"grad[{i}]")
+        # update gradients: the triangular term plus the square-mean term, added in bf16
+        # by autograd on both sides; gamma: a reduction over tokens
+        kind = "elementwise" if i == 0 else ("chained" if i < active + 1 else "reduced")
+        assert_parity(a, b, dtype if i < active + 1 else gdt, what=f"grad[{i}]", kind=kind)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -126,9 +134,9 @@ def test_fused_stage_schedule_and_all_gradients(dtype, slots, events):
     xc, ac, bc = _cpu_leaf(x), _cpu_leaf(alpha), _cpu_leaf(beta)
     ref = stage(xc, ac, bc, O.read, O.triangular_torch, O.write)
     rgrads = torch.autograd.grad(ref, (xc, ac, bc), go.cpu())
-    assert_parity(out, ref, dtype, what="stage out")
+    assert_parity(out, ref, dtype, what="stage out", kind="chained")
     for name, a, b in zip(("dX", "dalpha", "dbeta"), grads, rgrads):
-        assert_parity(a, b, dtype, what=name)
+        assert_parity(a, b, dtype, what=name, kind="chained" if name == "dX" else "reduced")
     if dtype == torch.float32:
         lit = O.literal_stage(xc.detach().double(), ac.detach().double(), bc.detach().double(),
                               [lambda z: 0.05 * z.tanh()] * events)

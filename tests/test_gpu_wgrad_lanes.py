@@ -35,7 +35,7 @@ def test_padded_event_lanes(active, channels, dtype):
     for j in range(active):
         assert torch.equal(ddz[j].cpu(), rdz[j]), f"update gradient {j} not bit-exact"
     wdt = torch.float32 if dtype == torch.float32 else dtype
-    assert_parity(dg, rdg, wdt, what="dgamma (fused)")
+    assert_parity(dg, rdg, wdt, what="dgamma (fused)", kind="reduced")
     gg = launch.triangular_gamma_grad(grad, ups, gamma, out_dtype=torch.float32)
-    assert_parity(gg, O.triangular_gamma_grad(grad.cpu(), [u.cpu() for u in ups]), wdt, what="dgamma")
+    assert_parity(gg, O.triangular_gamma_grad(grad.cpu(), [u.cpu() for u in ups]), wdt, what="dgamma", kind="reduced")
     assert torch.equal(gg, launch.triangular_gamma_grad(grad, ups, gamma, out_dtype=torch.float32))

@@ -182,6 +182,38 @@ def test_gather_scatter_round_trip_and_identity():
     assert torch.equal(O.gather_cells(x, ident, 4), O.high_to_cells(x, 4))
 
 
+def test_scatter_add_is_the_adjoint_of_the_gather():
+    """Pins oracle.scatter_add_cells: (1) small integers make every fp32 sum exact in any
+    order, so it must equal torch's index_add_ (a library scatter-add) bit for bit; (2)
+    <gather(x), g> == <x, scatter_add(g)> (the adjoint identity) in float64; (3) for a
+    permutation it equals the scatter copy, -0.0 included; (4) unselected states are +0."""
+    torch.manual_seed(11)
+    b, g, c = 3, 4, 6
+    idx = torch.randint(0, g * g, (b, g * g), dtype=torch.int32)
+    idx[:, :3] = 5  # a state selected three times in every row
+    grad = torch.randint(-8, 9, (b, g * g, 4, c)).float()
+    got = O.high_to_cells(O.scatter_add_cells(grad, idx), 4)
+    want = torch.zeros(b, g * g, 4, c)
+    for r in range(b):
+        want[r].index_add_(0, idx[r].long(), grad[r])
+    assert torch.equal(got, want)
+    x = torch.randn(b, 2 * g, 2 * g, c, dtype=torch.float64)
+    gg = torch.randn(b, g * g, 4, c, dtype=torch.float64)
+    lhs = (O.gather_cells(x, idx, 4) * gg).sum()
+    rhs = (x * O.scatter_add_cells(gg.float(), idx).double()).sum()
+    assert abs(float(lhs - rhs)) <= 1e-5 * float(gg.abs().sum())
+    perm = torch.stack([torch.randperm(g * g) for _ in range(b)]).to(torch.int32)
+    cells = torch.randn(b, g * g, 4, c).to(torch.bfloat16)
+    cells[0, 0, 0, 0] = -0.0
+    assert torch.equal(O.scatter_add_cells(cells, perm).view(torch.int16),
+                       O.scatter_cells(cells, perm).view(torch.int16))
+    unselected = torch.ones(g * g, dtype=torch.bool)
+    unselected[idx[0].long()] = False
+    out0 = O.high_to_cells(O.scatter_add_cells(grad, idx), 4)[0]
+    assert unselected.any() and (out0[unselected] == 0).all()
+    assert not torch.signbit(out0[unselected]).any()
+
+
 def test_planted_slot_swap_is_caught(monkeypatch):
     """A mistake planted in the oracle (slots ux/uy transposed) must fail the pins."""
     def swapped(x, slots):
