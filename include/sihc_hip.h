@@ -40,6 +40,8 @@ extern "C" {
 
 #define SIHC_MAX_EVENTS 32
 #define SIHC_ABI_VERSION 2
+/* Bytes of the per-GPU scratch array of sihc_event_backward_noalloc (64 MiB). */
+#define SIHC_SCRATCH_BYTES (64u << 20)
 
 enum { SIHC_DTYPE_F32 = 0, SIHC_DTYPE_BF16 = 1 };
 enum { SIHC_OK = 0, SIHC_ERR_INVALID = 1, SIHC_ERR_HIP = 2 };
@@ -145,6 +147,23 @@ int sihc_event_backward(const void *grad_x_out, const void *grad_z_out, const vo
                         int64_t batch, int grid, int cell, int channels,
                         const int32_t *index, int dtype, int w_dtype, void *workspace,
                         size_t workspace_bytes, void *stream);
+
+/* sihc_event_backward without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP-graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. Same arguments, checks, kernels and
+ * results (bit for bit) as sihc_event_backward; the partial rows of the weight-gradient
+ * reduction go to a file-scope device array of SIHC_SCRATCH_BYTES that each GPU holds
+ * until the process ends. Sizes whose partial rows exceed it
+ * (sihc_event_backward_workspace_size() > SIHC_SCRATCH_BYTES) are rejected with
+ * SIHC_ERR_INVALID before any launch. Calls no hipMalloc/hipFree. All calls on one GPU
+ * share its array: calls that overlap on one GPU (other streams, other threads) race and
+ * must be serialised by the caller. */
+int sihc_event_backward_noalloc(const void *grad_x_out, const void *grad_z_out,
+                                const void *x_out, const void *dz, const void *beta,
+                                const void *alpha_next, void *grad_x, void *grad_dz,
+                                void *grad_beta, void *grad_alpha_next, int64_t batch, int grid,
+                                int cell, int channels, const int32_t *index, int dtype,
+                                int w_dtype, void *stream);
 
 /* cells[b,n,s,c] = x[carrier pixel of slot s of cell index[b,n], c]: bit-exact copy of
  * each token's prediction state into a packed [batch, grid*grid, slots, channels] tile.

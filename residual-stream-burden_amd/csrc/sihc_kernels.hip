@@ -2075,6 +2075,44 @@ int event_vec(int C, int es, int cell, const void* const* ptrs, int n) {
 
 }  // namespace
 
+// ----------------------------------------------------------------------------------
+// Scratch of the allocation-free per-event backward (sihc_event_backward_noalloc): the
+// fp32 partial rows of its weight-gradient reduction. Every GPU the library runs on
+// holds its own copy of this array, at its own address, until the process ends. In host
+// code `scratch` names a host-side stand-in, never device memory: host code uses only
+// the per-device address that scratch_address() obtains from the runtime.
+// ----------------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[SIHC_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+
+// Device address of `scratch` on the current device, looked up once per device (with
+// that device current) and kept; SIHC_ERR_HIP if the runtime cannot resolve it.
+int scratch_address(const char* what, void** out) {
+  static std::mutex mu;
+  static void* addr[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return fail(SIHC_ERR_HIP, "%s: no current HIP device", what);
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return fail(SIHC_ERR_HIP, "%s: cannot resolve the scratch array on device %d: %s", what, dev,
+                  hipGetErrorString(err));
+    }
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return SIHC_OK;
+}
+
+}  // namespace
+
 // ==================================================================================
 // C ABI
 // ==================================================================================
@@ -2410,7 +2448,7 @@ size_t sihc_event_backward_workspace_size(int64_t batch, int grid, int cell, int
   return size_t(event_bwd_chunks(M)) * 2 * cell * cell * channels * sizeof(float);
 }
 
-// implementation of sihc_event_backward (errors name the entry point)
+// sihc_event_backward and its allocation-free variant (errors name the entry point)
 static int event_backward_impl(const char* what, const void* grad_x_out, const void* grad_z_out, const void* x_out,
                                const void* dz, const void* beta, const void* alpha_next, void* grad_x, void* grad_dz,
                                void* grad_beta, void* grad_alpha_next, int64_t batch, int grid, int cell,
@@ -2517,6 +2555,30 @@ int sihc_event_backward(const void* grad_x_out, const void* grad_z_out, const vo
   return event_backward_impl("sihc_event_backward", grad_x_out, grad_z_out, x_out, dz, beta, alpha_next, grad_x,
                              grad_dz, grad_beta, grad_alpha_next, batch, grid, cell, channels, index, dtype, w_dtype,
                              workspace, workspace_bytes, stream);
+}
+
+int sihc_event_backward_noalloc(const void* grad_x_out, const void* grad_z_out, const void* x_out, const void* dz,
+                                const void* beta, const void* alpha_next, void* grad_x, void* grad_dz,
+                                void* grad_beta, void* grad_alpha_next, int64_t batch, int grid, int cell,
+                                int channels, const int32_t* index, int dtype, int w_dtype, void* stream) {
+  const char* what = "sihc_event_backward_noalloc";
+  Geo g;
+  if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
+  // the partial rows the launch may use (its chunk count never exceeds this one)
+  const size_t need = size_t(event_bwd_chunks(g.M)) * 2 * cell * cell * size_t(channels) * sizeof(float);
+  if (need > size_t(SIHC_SCRATCH_BYTES))
+    return fail(SIHC_ERR_INVALID,
+                "%s: these sizes need %zu bytes of reduction scratch, more than the %zu-byte array this entry point "
+                "holds per GPU; use sihc_event_backward with a workspace",
+                what, need, size_t(SIHC_SCRATCH_BYTES));
+  void* ptr = nullptr;
+  if (g.M > 0)
+    if (int rc = scratch_address(what, &ptr)) return rc;
+  // same checks, kernels and reduction order as sihc_event_backward, with the scratch
+  // array as its workspace
+  return event_backward_impl(what, grad_x_out, grad_z_out, x_out, dz, beta, alpha_next, grad_x, grad_dz, grad_beta,
+                             grad_alpha_next, batch, grid, cell, channels, index, dtype, w_dtype, ptr,
+                             size_t(SIHC_SCRATCH_BYTES), stream);
 }
 
 int sihc_gather_cells(const void* x, const int32_t* index, void* cells, int64_t batch, int grid, int cell,
