@@ -106,7 +106,11 @@ class LiteralStep:
         self.galpha = torch.empty_like(self.alpha)
         self.gbeta = torch.empty_like(self.beta)
         nws = self.L.sihc_event_backward_workspace_size(B, G, K, C)
-        self.work = torch.empty((nws + 15) // 16 * 4, device=dev, dtype=torch.float32)
+        # one workspace per backward call: each keeps its partial rows until the one
+        # deferred finalize after the last event (E x 9.4 MB at the benchmark shape)
+        # (slot E: the first read's adjoint, whose rows must not overwrite event 0's)
+        self.work = [torch.empty((nws + 15) // 16 * 4, device=dev, dtype=torch.float32) for _ in range(E + 1)]
+        self.info = (ctypes.c_int * (2 * E + 2))()
         self.stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
         self._build(E)
 
@@ -115,7 +119,8 @@ class LiteralStep:
         vp = ctypes.c_void_p
         p = lambda t: vp(t.data_ptr())  # noqa: E731
         bf16 = 1
-        work, nwork = p(self.work), self.work.numel() * 4
+        nwork = self.work[0].numel() * 4
+        info = lambda k: ctypes.cast(ctypes.addressof(self.info) + 8 * k, ctypes.POINTER(ctypes.c_int))  # noqa: E731
         U = self.M * C * ELEM
         S = self.S
         w_bytes = C * S * ELEM
@@ -126,43 +131,61 @@ class LiteralStep:
                                            self.stream), (S + 1) * U + w_bytes))
         for i in range(E):
             last = i == E - 1
-            fwd.append(("event_forward", L.sihc_event_forward,
+            fwd.append(("event_forward_last" if last else "event_forward", L.sihc_event_forward,
                         (p(self.x[i]), p(self.dz[i]), p(self.beta[i]), None if last else p(self.alpha[i + 1]),
                          p(self.x[i + 1]), None if last else p(self.z[i + 1]), B, G, K, C, None, bf16, self.stream),
                         ((2 * S + 1) if last else (2 * S + 2)) * U + (1 if last else 2) * w_bytes))
-        # backward: last event (write only, carrier gradient aliased), then full events
+        # backward: last event (write only, carrier gradient aliased), then full events, each
+        # with its weight-gradient finalize deferred (sihc_event_backward_partial) ...
         h = self.h_out
-        bwd.append(("event_backward_last", L.sihc_event_backward,
+        bwd.append(("event_backward_last", L.sihc_event_backward_partial,
                     (p(h), None, None, p(self.dz[E - 1]), p(self.beta[E - 1]), None, None, p(self.gdz[E - 1]),
-                     p(self.gbeta[E - 1]), None, B, G, K, C, None, bf16, bf16, work, nwork, self.stream),
-                    (S + 2) * U + 2 * w_bytes))
+                     p(self.gbeta[E - 1]), None, B, G, K, C, None, bf16, bf16, p(self.work[E - 1]), nwork, info(E - 1),
+                     self.stream), (S + 2) * U + 2 * w_bytes))
         for i in range(E - 2, -1, -1):
             dst = self.gx[i % 2]
-            bwd.append(("event_backward", L.sihc_event_backward,
+            bwd.append(("event_backward", L.sihc_event_backward_partial,
                         (p(h), p(self.gz[i + 1]), p(self.x[i + 1]), p(self.dz[i]), p(self.beta[i]),
                          p(self.alpha[i + 1]), p(dst), p(self.gdz[i]), p(self.gbeta[i]), p(self.galpha[i + 1]),
-                         B, G, K, C, None, bf16, bf16, work, nwork, self.stream),
+                         B, G, K, C, None, bf16, bf16, p(self.work[i]), nwork, info(i), self.stream),
                         (3 * S + 3) * U + 4 * w_bytes))
             h = dst
         # adjoint of the first read (no write part): dX_0 = h + alpha_0 (x) g_0, dalpha_0
         dst = self.gx[1] if h is self.gx[0] else self.gx[0]
-        bwd.append(("event_backward_first", L.sihc_event_backward,
+        bwd.append(("event_backward_first", L.sihc_event_backward_partial,
                     (p(h), p(self.gz[0]), p(self.x[0]), None, None, p(self.alpha[0]), p(dst), None, None,
-                     p(self.galpha[0]), B, G, K, C, None, bf16, bf16, work, nwork, self.stream),
-                    (3 * S + 1) * U + 2 * w_bytes))
+                     p(self.galpha[0]), B, G, K, C, None, bf16, bf16, p(self.work[E]), nwork, info(E),
+                     self.stream), (3 * S + 1) * U + 2 * w_bytes))
+        # ... then every event's dbeta / dalpha in one launch per 32 events (same bits)
+        self.finalize_args = None
+        bwd.append(("event_finalize", self._finalize, (), 0))
         self.fwd, self.bwd = fwd, bwd
         self.bytes_fwd = sum(c[3] for c in fwd)
         self.bytes_bwd = sum(c[3] for c in bwd)
 
+    def _finalize(self):
+        """sihc_event_finalize over the E + 1 deferred backward calls: slot i < E holds
+        event i's dbeta_i (and dalpha_{i+1}, except the last event's write-only slot); slot
+        E the first read's dalpha_0. The info slots were filled by the calls this step."""
+        if self.finalize_args is None:
+            E = self.E
+            ptrs = lambda ts: (ctypes.c_void_p * len(ts))(*(None if t is None else t.data_ptr() for t in ts))  # noqa
+            self.finalize_args = (E + 1, ptrs(self.work), self.info, ptrs([self.gbeta[i] for i in range(E)] + [None]),
+                                  ptrs([self.galpha[i + 1] for i in range(E - 1)] + [None, self.galpha[0]]),
+                                  self.K, self.C, 1, self.stream)
+        return self.L.sihc_event_finalize(*self.finalize_args)
+
     def run(self, calls, timer=None):
+        """Launch a call list; with `timer` (a dict), HIP events on the launch stream around
+        every full per-event forward and backward launch go to timer[name]."""
         for name, fn, args, _ in calls:
-            if timer is not None and name == "event_backward":
+            if timer is not None and name in ("event_forward", "event_backward"):
                 start = self.torch.cuda.Event(enable_timing=True)
                 end = self.torch.cuda.Event(enable_timing=True)
                 start.record()
                 self.check(fn(*args))
                 end.record()
-                timer.append((start, end))
+                timer.setdefault(name, []).append((start, end))
             else:
                 self.check(fn(*args))
 
@@ -184,20 +207,53 @@ def _timed(torch, fn, iters=10, warmup=2):
     return a.elapsed_time(b) / iters * 1e-3
 
 
-def copy_ceiling() -> dict:
-    """The library's 16-byte grid-stride copy of 1 GiB on the same GPU in the same run:
-    a plain 1:1 read/write stream, the context for the per-event kernels' fraction of
-    the nominal 8 TB/s (the per-event backward moves 10 units read : 5 written)."""
+def stream_ceiling() -> dict:
+    """HBM streaming ceiling of this GPU in the same run: the library's calibration stream
+    (sihc_stream: grid-stride 16-byte vectors, non-temporal loads and stores, the hints of
+    the per-event kernels) over at least 8 GiB per pass, for the read:write mixes and array
+    counts of the per-event kernels -- forward 1:1 over 4 arrays (x, dz in; x_out, z_out
+    out), backward 2:1 over 6 arrays (dX', dz', X', dz in; dX, ddz out) -- plus 1:1 over
+    2 arrays, 2:1 over 3 and write-only. Best of two grid sizes, median of 3 passes."""
     import torch
 
-    from sihc_hip import launch
+    from sihc_hip import _lib
 
-    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
-    dst = torch.empty_like(src)
-    sec = _timed(torch, lambda: launch.copy_(dst, src), iters=20, warmup=3)
-    gbs = 2 * src.numel() / sec / 1e9
-    return {"workload": "1 GiB copy (1 GiB read + 1 GiB written), 16-byte vectors", "ms": round(sec * 1e3, 3),
-            "GB/s": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    L = _lib.lib()
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    mixes = {"write-only (1 array)": (0, 1, 8 << 30), "1:1 (2 arrays)": (1, 1, 4 << 30),
+             "2:1 (3 arrays)": (2, 1, 3 << 30), "1:1 (4 arrays, the per-event forward's mix)": (2, 2, 2 << 30),
+             "2:1 (6 arrays, the per-event backward's mix)": (4, 2, 3 << 29)}
+    pool_bytes = max((nr + nw) * each for nr, nw, each in mixes.values())
+    pool = torch.empty(pool_bytes, dtype=torch.uint8, device="cuda")
+    pool.fill_(1)
+    out = {"workload": "sihc_stream over >= 8 GiB per pass (read + written), non-temporal loads and stores"}
+    for name, (nr, nw, each) in mixes.items():
+        arrays = [pool[k * each:(k + 1) * each] for k in range(nr + nw)]
+        # the kernel streams `each` bytes of every array: each slice must hold exactly that
+        if any(a.numel() != each for a in arrays):
+            raise RuntimeError(f"stream_ceiling: pool of {pool_bytes} bytes too small for {name}")
+        srcs = (ctypes.c_void_p * max(nr, 1))(*[a.data_ptr() for a in arrays[:nr]])
+        dsts = (ctypes.c_void_p * nw)(*[a.data_ptr() for a in arrays[nr:]])
+        best = None
+        for blocks in (4096, 16384):
+            fn = lambda: _lib.check(L.sihc_stream(srcs, nr, dsts, nw, each, blocks, st))  # noqa: E731
+            passes = []
+            for _ in range(4):
+                a0, b0 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a0.record()
+                fn()
+                b0.record()
+                torch.cuda.synchronize()
+                passes.append(a0.elapsed_time(b0) * 1e-3)
+            sec = statistics.median(passes[1:])
+            gbs = (nr + nw) * each / sec / 1e9
+            if best is None or gbs > best[0]:
+                best = (gbs, blocks, sec)
+        out[name] = {"GB/s": round(best[0], 1), "frac_of_peak": round(best[0] / HBM_PEAK_GBS, 4),
+                     "bytes_per_pass": (nr + nw) * each, "ms": round(best[2] * 1e3, 3), "blocks": best[1]}
+    del pool
+    torch.cuda.empty_cache()
+    return out
 
 
 def extra_configs(seed: int) -> dict:
@@ -310,6 +366,70 @@ def extra_configs(seed: int) -> dict:
     return out
 
 
+def stage_api_config2(seed: int, steps: int = 3) -> dict:
+    """Benchmark config 2 on the reference's own schedule (sublayer.py:52-72), the drop-in
+    path: per stage of 8/12/8 blocks (16/24/16 events) read -> triangular -> write through
+    the sihc:: custom ops, then torch autograd back through them, batch 256, D = 1152, bf16.
+    As in the per-event leg the sublayer bodies are not part of the path: the updates dz_i
+    are pre-drawn leaves and the bodies' input gradients g_i = dL/dz_i are pre-drawn upstream
+    gradients of the read outputs z_i. Bytes: the algorithmic bytes of the kernel ops
+    launched (read (S+E), triangular i (i+2), write (2S+E); backward: update reads and the
+    weight gradients (S+E) each, fused triangular backward (1+2i)); the time also covers
+    autograd's own work (gamma products, gradient accumulation in bf16)."""
+    import torch
+
+    from sihc_hip.sublayer_kernels import sublayer_read, sublayer_triangular, sublayer_write
+
+    dev = torch.device("cuda", 0)
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(seed)
+    r = lambda shape, m=0.0, sd=1.0: (m + sd * torch.randn(shape, device=dev, generator=g)).to(bf)  # noqa: E731
+    B, C, S = 256, 1152, 4
+    U = B * 256 * C * ELEM
+    stages = (16, 24, 16)
+    x0 = r((B, 32, 32, C)).requires_grad_()
+    alphas = [r((e, C, S), 0.25, 0.02).requires_grad_() for e in stages]
+    betas = [r((e, C, S), 1.0, 0.02).requires_grad_() for e in stages]
+    dzs = [[r((B, 256, C)).requires_grad_() for _ in range(e)] for e in stages]
+    gzs = [[r((B, 256, C), 0.0, 1e-2) for _ in range(e)] for e in stages]
+    g_out = r((B, 32, 32, C), 0.0, 1e-2)
+
+    def run():
+        x = x0
+        outs, grads = [], []
+        for alpha, beta, dz, gz in zip(alphas, betas, dzs, gzs):
+            base = sublayer_read(x, alpha)
+            gamma = (alpha[:, None] * beta[None, :]).sum(-1)
+            for i in range(len(dz)):
+                z = base[i] if i == 0 else sublayer_triangular(base[i], dz[:i], gamma[i, :i].contiguous())
+                outs.append(z)
+                grads.append(gz[i])
+            x = sublayer_write(x, dz, beta)
+        torch.autograd.backward(outs + [x], grads + [g_out])
+
+    fwd_u = sum((S + e) + sum(i + 2 for i in range(1, e)) + (2 * S + e) for e in stages)
+    bwd_u = sum(4 * (S + e) + sum(1 + 2 * i for i in range(1, e)) for e in stages)
+    for _ in range(1):
+        run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        for t in [x0, *alphas, *betas, *(d for ds in dzs for d in ds)]:
+            t.grad = None
+        run()
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / steps
+    nbytes = (fwd_u + bwd_u) * U
+    out = {"workload": "benchmark config 2 on the reference's stage schedule (read -> triangular -> write, stages "
+                       "8/12/8) through the sihc:: custom ops, fwd + autograd bwd, batch 256, D=1152, bf16",
+           "ms_per_step": round(sec * 1e3, 3), "kernel_op_bytes": nbytes, "fwd_units": fwd_u, "bwd_units": bwd_u,
+           "GB/s": round(nbytes / sec / 1e9, 1), "frac_of_peak": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
+           "tokens_per_s": round(B * 256 / sec, 1)}
+    del x0, alphas, betas, dzs, gzs, g_out
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(budget_s: float) -> dict:
     """benchmark config 0 on the host: the oracle's unfused PyTorch read/write (fp32,
     batch 8, 256 tokens, 4 slots, D=768, one event) forward + autograd backward."""
@@ -393,7 +513,7 @@ def calibrate(args) -> None:
     B, G, K, C = step.B, step.G, step.K, step.C
     bwd_args = (p(step.h_out), p(step.gz[1]), p(step.x[1]), p(step.dz[0]), p(step.beta[0]), p(step.alpha[1]),
                 p(step.gx[0]), p(step.gdz[0]), p(step.gbeta[0]), p(step.galpha[1]), B, G, K, C, None, 1, 1,
-                p(step.work), step.work.numel() * 4, step.stream)
+                p(step.work[0]), step.work[0].numel() * 4, step.stream)
     for _ in range(3):
         check(fwd[1](*fwd[2]))
     for _ in range(3):
@@ -701,7 +821,7 @@ def main():
     torch.cuda.synchronize()
     print(f"[bench] warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
 
-    timer: list = []
+    timer: dict = {}
     t_fwd: list = []
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     torch.cuda.synchronize()
@@ -709,7 +829,7 @@ def main():
     for _ in range(args.steps):
         a, b, c = ev(), ev(), ev()
         a.record()
-        step.run(step.fwd)
+        step.run(step.fwd, timer)
         b.record()
         step.run(step.bwd, timer)
         c.record()
@@ -719,14 +839,18 @@ def main():
     ms_step = wall / args.steps * 1e3
     fwd_ms = statistics.median(a.elapsed_time(b) for a, b, _ in t_fwd)
     bwd_ms = statistics.median(b.elapsed_time(c) for _, b, c in t_fwd)
-    kern_ms = [s.elapsed_time(e) for s, e in timer]
+    kern_ms = [s.elapsed_time(e) for s, e in timer["event_backward"]]
     avg_kernel_ms = sum(kern_ms) / len(kern_ms)
+    fwd_kern_ms = [s.elapsed_time(e) for s, e in timer["event_forward"]]
+    avg_fwd_kernel_ms = sum(fwd_kern_ms) / len(fwd_kern_ms)
     print(f"[bench] timed {args.steps} steps: {ms_step:.3f} ms/step", file=sys.stderr, flush=True)
 
     total_bytes = step.bytes_fwd + step.bytes_bwd
     gbs = total_bytes / (ms_step * 1e-3) / 1e9
     dom_bytes = next(c[3] for c in step.bwd if c[0] == "event_backward")
     achieved = dom_bytes / (avg_kernel_ms * 1e-3) / 1e9
+    fwd_bytes = next(c[3] for c in step.fwd if c[0] == "event_forward")
+    fwd_rate = fwd_bytes / (avg_fwd_kernel_ms * 1e-3) / 1e9
     traffic = traffic_from_profiles()
     result = {
         "metric": METRIC,
@@ -749,17 +873,23 @@ def main():
         },
         "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(args.batch * 256 / (ms_step * 1e-3), 1),
+        "fwd_kernel_GBps": round(fwd_rate, 1),
+        "fwd_kernel_avg_ms": round(avg_fwd_kernel_ms, 4),
         "fwd_ms": round(fwd_ms, 3),
         "bwd_ms": round(bwd_ms, 3),
         "algorithmic_bytes_per_step": total_bytes,
         "roofline": {
-            "kernel": "k_event_bwd (sihc_event_backward, full event) incl. its partial-sum finalize",
+            "kernel": "k_event_bwd (sihc_event_backward_partial, full event; the step's one deferred "
+                      "finalize of all events is outside the launch)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": ("committed profiles/event_backward_traffic.json: rocprofv3 FETCH_SIZE + WRITE_SIZE "
+                               "of bench.py --mode calibrate, scaled by the same counters on the library's copy "
+                               "of 1 GiB; not measured in this run") if traffic is not None else None,
             "bytes_per_launch": dom_bytes,
             "avg_launch_ms": round(avg_kernel_ms, 4),
             "launches": len(kern_ms),
@@ -770,7 +900,14 @@ def main():
         torch.cuda.empty_cache()
         print("[bench] secondary configs 1 and 3", file=sys.stderr, flush=True)
         result["extra"] = extra_configs(args.seed)
-        result["extra"]["copy_ceiling"] = copy_ceiling()
+        print("[bench] config 2 on the stage API (drop-in path)", file=sys.stderr, flush=True)
+        result["extra"]["config2_stage_api"] = stage_api_config2(args.seed)
+        result["extra"]["stream_ceiling"] = ceiling = stream_ceiling()
+        fw_rate = result["fwd_kernel_GBps"]
+        result["extra"]["fraction_of_stream_ceiling"] = {
+            "k_event_fwd vs 1:1 over 4 arrays": round(fw_rate / ceiling["1:1 (4 arrays, the per-event forward's mix)"]["GB/s"], 4),
+            "k_event_bwd vs 2:1 over 6 arrays": round(achieved / ceiling["2:1 (6 arrays, the per-event backward's mix)"]["GB/s"], 4),
+        }
         torch.cuda.empty_cache()
         print("[bench] config 4 end-to-end forward", file=sys.stderr, flush=True)
         result["extra"]["config4_e2e"] = e2e_config4(args.seed)

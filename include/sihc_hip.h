@@ -148,6 +148,29 @@ int sihc_event_backward(const void *grad_x_out, const void *grad_z_out, const vo
                         const int32_t *index, int dtype, int w_dtype, void *workspace,
                         size_t workspace_bytes, void *stream);
 
+/* sihc_event_backward with its weight-gradient finalize deferred, so the finalizes of a
+ * chain of events can run as one launch (sihc_event_finalize) after the last of them:
+ * the kernel leaves its partial rows in `workspace` (which must then stay untouched until
+ * the finalize) and writes, on the host, info[0] = the number of partial rows and info[1]
+ * = which gradients they hold (bit 0 grad_beta, bit 1 grad_alpha_next). A grad_alpha_next
+ * without a read part is zeroed here, as sihc_event_backward does. Same kernels and, after
+ * the finalize, the same bits as sihc_event_backward.
+ * No reference counterpart (a launch schedule of the per-event backward). */
+int sihc_event_backward_partial(const void *grad_x_out, const void *grad_z_out,
+                                const void *x_out, const void *dz, const void *beta,
+                                const void *alpha_next, void *grad_x, void *grad_dz,
+                                void *grad_beta, void *grad_alpha_next, int64_t batch, int grid,
+                                int cell, int channels, const int32_t *index, int dtype,
+                                int w_dtype, void *workspace, size_t workspace_bytes, int *info,
+                                void *stream);
+/* The deferred finalizes of n sihc_event_backward_partial calls (host arrays of n
+ * workspaces, 2n info ints and n gradient pointers each, as passed to those calls; a
+ * gradient the info does not list may be NULL): the fixed-order partial sums of each
+ * event, stored in w_dtype. One launch per 32 events. */
+int sihc_event_finalize(int n, const void *const *workspaces, const int *info,
+                        void *const *grad_beta, void *const *grad_alpha_next, int cell,
+                        int channels, int w_dtype, void *stream);
+
 /* sihc_event_backward without a workspace argument, for callers that cannot allocate
  * device memory (code under HIP-graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). No counterpart in the reference. Same arguments, checks, kernels and
@@ -184,6 +207,15 @@ int sihc_scatter_cells(const void *cells, const int32_t *index, void *x, int64_t
  * No reference counterpart (the backward of the spatially indexed gather). */
 int sihc_scatter_add_cells(const void *cells, const int32_t *index, void *x, int64_t batch,
                            int grid, int cell, int channels, int dtype, void *stream);
+
+/* Streaming calibration: reads nsrc arrays and writes ndst arrays of `bytes` bytes each
+ * (16-byte aligned, bytes a multiple of 16) with a grid-stride loop of `blocks` 256-thread
+ * blocks and non-temporal loads and stores; dst_j = XOR of the sources ^ j (write-only:
+ * an index pattern). Mixes 0:1, 1:1, 2:1, 2:2 and 4:2 (the per-event kernels move their
+ * bytes 1:1 and 2:1 over 4 and 6 arrays). No reference counterpart: the HBM ceiling the per-event kernels are read
+ * against. */
+int sihc_stream(const void *const *src, int nsrc, void *const *dst, int ndst, size_t bytes,
+                int blocks, void *stream);
 
 /* Plain device copy of `bytes` bytes (16-byte vectors). No reference counterpart: it is
  * the calibration kernel for HBM counters and the practical bandwidth ceiling. */

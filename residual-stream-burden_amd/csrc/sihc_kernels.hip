@@ -63,6 +63,9 @@
 #ifndef SIHC_EV_CHUNK  // tokens per reduction chunk, per-event backward
 #define SIHC_EV_CHUNK 256
 #endif
+#ifndef SIHC_EV_MAXCHUNKS  // most reduction chunks (partial rows) of the per-event backward
+#define SIHC_EV_MAXCHUNKS 512
+#endif
 #ifndef SIHC_EV_GROUP  // tokens per interleaved group of a backward chunk (0: contiguous)
 #define SIHC_EV_GROUP 32
 #endif
@@ -1139,14 +1142,14 @@ __global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgradz(const bf16_t* __
 // then the 8 group sums are added in ascending group order.
 // ----------------------------------------------------------------------------------
 template <typename TO>
-__global__ void __launch_bounds__(256) k_finalize(const float* __restrict__ part, TO* __restrict__ out0,
-                                                  TO* __restrict__ out1, int chunks, int R, int S, int C,
-                                                  int pair, int zero_mask) {
+__device__ __forceinline__ void finalize_outputs(const float* __restrict__ part, TO* __restrict__ out0,
+                                                 TO* __restrict__ out1, int chunks, int R, int S, int C, int pair,
+                                                 int zero_mask, int block) {
   constexpr int FO = 32, FG = 8;
   __shared__ float red[FG][FO];
   const int64_t n = int64_t(R) * S * C;
   const int o = threadIdx.x % FO, grp = threadIdx.x / FO;
-  const int64_t i = int64_t(blockIdx.x) * FO + o;
+  const int64_t i = int64_t(block) * FO + o;
   const int r = i < n ? int(i / (int64_t(S) * C)) : 0;
   const bool zero = (zero_mask >> r) & 1;
   float sum = 0.f;
@@ -1173,6 +1176,31 @@ __global__ void __launch_bounds__(256) k_finalize(const float* __restrict__ part
   const int c = rem - s * C;
   TO* dst = pair ? (r == 0 ? out0 : out1) : (out0 ? out0 + int64_t(r) * C * S : nullptr);
   if (dst) dst[int64_t(c) * S + s] = from_f32<TO>(zero ? 0.f : t);
+}
+
+template <typename TO>
+__global__ void __launch_bounds__(256) k_finalize(const float* __restrict__ part, TO* __restrict__ out0,
+                                                  TO* __restrict__ out1, int chunks, int R, int S, int C,
+                                                  int pair, int zero_mask) {
+  finalize_outputs<TO>(part, out0, out1, chunks, R, S, C, pair, zero_mask, int(blockIdx.x));
+}
+
+// The per-event backward's finalize for up to SIHC_FINALIZE_BATCH deferred events in one
+// launch (grid.y = event): the same fixed-order sums as k_finalize, so the same bits.
+#define SIHC_FINALIZE_BATCH 32
+struct FinalizeBatch {
+  const float* part[SIHC_FINALIZE_BATCH];
+  void* out0[SIHC_FINALIZE_BATCH];
+  void* out1[SIHC_FINALIZE_BATCH];
+  int chunks[SIHC_FINALIZE_BATCH];
+  int zero_mask[SIHC_FINALIZE_BATCH];
+};
+
+template <typename TO>
+__global__ void __launch_bounds__(256) k_finalize_batch(FinalizeBatch b, int S, int C) {
+  const int e = int(blockIdx.y);
+  finalize_outputs<TO>(b.part[e], static_cast<TO*>(b.out0[e]), static_cast<TO*>(b.out1[e]), b.chunks[e], 2, S, C,
+                       1, b.zero_mask[e], int(blockIdx.x));
 }
 
 template <typename TO>
@@ -1535,6 +1563,24 @@ __global__ void __launch_bounds__(256) k_copy16(const u32x4* __restrict__ src, u
     st<NTS>(dst + i, ld<NTL>(src + i));
 }
 
+// Streaming calibration: NR arrays read and NW arrays written, n 16-byte vectors each,
+// grid-stride, non-temporal loads and stores (the hints of the per-event kernels); each
+// output is the XOR of the inputs (and its own index), so no load can be skipped.
+template <int NR, int NW>
+__global__ void __launch_bounds__(256) k_stream(PtrPack src, PtrPack dst, int64_t n) {
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+    u32x4 acc = {uint32_t(i), uint32_t(i >> 32), 0u, 0u};  // write-only: the index pattern
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const u32x4 v = ld<true>(static_cast<const u32x4*>(src.p[r]) + i);
+      acc = r == 0 ? v : (acc ^ v);
+    }
+#pragma unroll
+    for (int w = 0; w < NW; ++w) st<true>(static_cast<u32x4*>(const_cast<void*>(dst.p[w])) + i, acc ^ uint32_t(w));
+  }
+}
+
 __global__ void k_copy1(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t n) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) dst[i] = src[i];
@@ -1645,7 +1691,7 @@ int wgrad_chunks(int64_t M, int events, int C) {
   const int64_t cap = std::max<int64_t>(1, std::min<int64_t>(M / 32, 2048));
   return int(std::max<int64_t>(base, std::min(want, cap)));
 }
-int event_bwd_chunks(int64_t M) { return chunk_count(M, SIHC_EV_CHUNK, 512); }
+int event_bwd_chunks(int64_t M) { return chunk_count(M, SIHC_EV_CHUNK, SIHC_EV_MAXCHUNKS); }
 // Token chunks of the fused triangular backward (which also stores the update
 // gradients): one per SIHC_TRIB_CHUNK tokens up to 1024, at least the weight-gradient
 // count. Shorter runs per block stream through a narrower window of each array (A = 3:
@@ -2453,7 +2499,7 @@ static int event_backward_impl(const char* what, const void* grad_x_out, const v
                                const void* dz, const void* beta, const void* alpha_next, void* grad_x, void* grad_dz,
                                void* grad_beta, void* grad_alpha_next, int64_t batch, int grid, int cell,
                                int channels, const int32_t* index, int dtype, int w_dtype, void* workspace,
-                               size_t workspace_bytes, void* stream) {
+                               size_t workspace_bytes, void* stream, int* defer = nullptr) {
   Geo g;
   if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
   if (!valid_dtype(dtype) || !valid_dtype(w_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
@@ -2465,6 +2511,7 @@ static int event_backward_impl(const char* what, const void* grad_x_out, const v
   const int64_t wn = int64_t(S) * channels;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (g.M == 0) {  // no tokens: zero weight gradients (token tensors may carry NULL pointers)
+    if (defer) defer[0] = defer[1] = 0;  // nothing left for the finalize
     if (beta && grad_beta)
       if (int rc = fill_zero(w_dtype, grad_beta, wn, st, what)) return rc;
     if (grad_alpha_next) return fill_zero(w_dtype, grad_alpha_next, wn, st, what);
@@ -2540,6 +2587,12 @@ static int event_backward_impl(const char* what, const void* grad_x_out, const v
     });
   });
   if (rc) return rc;
+  if (defer) {  // the caller runs the finalize later (sihc_event_finalize)
+    defer[0] = chunks;
+    defer[1] = (has_w ? 1 : 0) | (has_g ? 2 : 0);
+    if (!has_g && grad_alpha_next) return fill_zero(w_dtype, grad_alpha_next, wn, st, what);
+    return SIHC_OK;
+  }
   // Partial rows are [chunks][2][S][C]: row 0 -> grad_beta, row 1 -> grad_alpha_next
   // (written as zeros when there is no read part). A part the kernel did not run has no
   // partial rows, so the finalize does not read them.
@@ -2555,6 +2608,62 @@ int sihc_event_backward(const void* grad_x_out, const void* grad_z_out, const vo
   return event_backward_impl("sihc_event_backward", grad_x_out, grad_z_out, x_out, dz, beta, alpha_next, grad_x,
                              grad_dz, grad_beta, grad_alpha_next, batch, grid, cell, channels, index, dtype, w_dtype,
                              workspace, workspace_bytes, stream);
+}
+
+int sihc_event_backward_partial(const void* grad_x_out, const void* grad_z_out, const void* x_out, const void* dz,
+                                const void* beta, const void* alpha_next, void* grad_x, void* grad_dz,
+                                void* grad_beta, void* grad_alpha_next, int64_t batch, int grid, int cell,
+                                int channels, const int32_t* index, int dtype, int w_dtype, void* workspace,
+                                size_t workspace_bytes, int* info, void* stream) {
+  const char* what = "sihc_event_backward_partial";
+  if (!info) return fail(SIHC_ERR_INVALID, "%s: null info", what);
+  return event_backward_impl(what, grad_x_out, grad_z_out, x_out, dz, beta, alpha_next, grad_x, grad_dz, grad_beta,
+                             grad_alpha_next, batch, grid, cell, channels, index, dtype, w_dtype, workspace,
+                             workspace_bytes, stream, info);
+}
+
+int sihc_event_finalize(int n, const void* const* workspaces, const int* info, void* const* grad_beta,
+                        void* const* grad_alpha_next, int cell, int channels, int w_dtype, void* stream) {
+  const char* what = "sihc_event_finalize";
+  if (n < 0 || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
+  if (cell != 2 && cell != 4) return fail(SIHC_ERR_INVALID, "%s: cell must be 2 or 4 (4 or 16 slots)", what);
+  if (!valid_dtype(w_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype %d", what, w_dtype);
+  if (n == 0) return SIHC_OK;
+  if (!workspaces || !info || !grad_beta || !grad_alpha_next) return fail(SIHC_ERR_INVALID, "%s: null array", what);
+  const int S = cell * cell;
+  // validate everything before the first launch
+  for (int i = 0; i < n; ++i) {
+    const int chunks = info[2 * i], rows = info[2 * i + 1];
+    if (chunks < 0 || rows < 0 || rows > 3) return fail(SIHC_ERR_INVALID, "%s: bad info of event %d", what, i);
+    if (chunks == 0 || rows == 0) continue;
+    if (!workspaces[i]) return fail(SIHC_ERR_INVALID, "%s: null workspace of event %d", what, i);
+    if (((rows & 1) && !grad_beta[i]) || ((rows & 2) && !grad_alpha_next[i]))
+      return fail(SIHC_ERR_INVALID, "%s: null gradient of event %d", what, i);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned bx = unsigned((int64_t(2) * S * channels + 31) / 32);
+  for (int i0 = 0; i0 < n; i0 += SIHC_FINALIZE_BATCH) {
+    FinalizeBatch b{};
+    int nb = 0;
+    for (int i = i0; i < std::min(n, i0 + SIHC_FINALIZE_BATCH); ++i) {
+      const int chunks = info[2 * i], rows = info[2 * i + 1];
+      if (chunks == 0 || rows == 0) continue;
+      b.part[nb] = static_cast<const float*>(workspaces[i]);
+      b.out0[nb] = (rows & 1) ? grad_beta[i] : nullptr;
+      b.out1[nb] = (rows & 2) ? grad_alpha_next[i] : nullptr;
+      b.chunks[nb] = chunks;
+      b.zero_mask[nb] = ((rows & 1) ? 0 : 1) | ((rows & 2) ? 0 : 2);  // rows without partials: not read
+      ++nb;
+    }
+    if (nb == 0) continue;
+    if (w_dtype == SIHC_DTYPE_F32) {
+      hipLaunchKernelGGL((k_finalize_batch<float>), dim3(bx, unsigned(nb)), dim3(256), 0, st, b, S, channels);
+    } else {
+      hipLaunchKernelGGL((k_finalize_batch<bf16_t>), dim3(bx, unsigned(nb)), dim3(256), 0, st, b, S, channels);
+    }
+    if (int rc = check_launch(what)) return rc;
+  }
+  return SIHC_OK;
 }
 
 int sihc_event_backward_noalloc(const void* grad_x_out, const void* grad_z_out, const void* x_out, const void* dz,
@@ -2594,6 +2703,37 @@ int sihc_scatter_cells(const void* cells, const int32_t* index, void* x, int64_t
 int sihc_scatter_add_cells(const void* cells, const int32_t* index, void* x, int64_t batch, int grid, int cell,
                            int channels, int dtype, void* stream) {
   return cells_add("sihc_scatter_add_cells", cells, index, x, batch, grid, cell, channels, dtype, stream);
+}
+
+int sihc_stream(const void* const* src, int nsrc, void* const* dst, int ndst, size_t bytes, int blocks,
+                void* stream) {
+  const char* what = "sihc_stream";
+  if (bytes == 0) return SIHC_OK;
+  if ((nsrc > 0 && !src) || !dst) return fail(SIHC_ERR_INVALID, "%s: null array", what);
+  if (bytes % 16) return fail(SIHC_ERR_INVALID, "%s: bytes must be a multiple of 16", what);
+  if (blocks < 1) return fail(SIHC_ERR_INVALID, "%s: blocks must be positive", what);
+  if (!((nsrc == 0 && ndst == 1) || (nsrc == 1 && ndst == 1) || (nsrc == 2 && ndst == 1) ||
+        (nsrc == 2 && ndst == 2) || (nsrc == 4 && ndst == 2)))
+    return fail(SIHC_ERR_INVALID, "%s: unsupported mix %d:%d (0:1, 1:1, 2:1, 2:2, 4:2)", what, nsrc, ndst);
+  for (int i = 0; i < nsrc; ++i)
+    if (!src[i] || !aligned(src[i], 16)) return fail(SIHC_ERR_INVALID, "%s: source %d null or misaligned", what, i);
+  for (int i = 0; i < ndst; ++i)
+    if (!dst[i] || !aligned(dst[i], 16)) return fail(SIHC_ERR_INVALID, "%s: destination %d null or misaligned", what, i);
+  PtrPack ps{}, pd{};
+  for (int i = 0; i < nsrc; ++i) ps.p[i] = src[i];
+  for (int i = 0; i < ndst; ++i) pd.p[i] = dst[i];
+  const int64_t n = int64_t(bytes / 16);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(unsigned(blocks)), dim3(256), 0, st, ps, pd, n);
+    return check_launch(what);
+  };
+  if (nsrc == 1 && ndst == 1) return go(k_stream<1, 1>);
+  if (nsrc == 2 && ndst == 1) return go(k_stream<2, 1>);
+  if (nsrc == 2 && ndst == 2) return go(k_stream<2, 2>);
+  if (nsrc == 4 && ndst == 2) return go(k_stream<4, 2>);
+  if (nsrc == 0 && ndst == 1) return go(k_stream<0, 1>);
+  return fail(SIHC_ERR_INVALID, "%s: unsupported mix %d:%d (0:1, 1:1, 2:1, 2:2, 4:2)", what, nsrc, ndst);
 }
 
 int sihc_copy(const void* src, void* dst, size_t bytes, void* stream) {

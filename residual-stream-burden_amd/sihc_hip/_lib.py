@@ -38,11 +38,16 @@ PROTOTYPES: dict[str, tuple] = {
     "sihc_event_backward_workspace_size": (_sz, [_i64, _i32, _i32, _i32]),
     "sihc_event_backward": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                    _i64, _i32, _i32, _i32, _vp, _i32, _i32, _vp, _sz, _vp]),
+    "sihc_event_backward_partial": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                           _i64, _i32, _i32, _i32, _vp, _i32, _i32, _vp, _sz,
+                                           ctypes.POINTER(ctypes.c_int), _vp]),
+    "sihc_event_finalize": (_i32, [_i32, _vpp, ctypes.POINTER(ctypes.c_int), _vpp, _vpp, _i32, _i32, _i32, _vp]),
     "sihc_event_backward_noalloc": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                            _i64, _i32, _i32, _i32, _vp, _i32, _i32, _vp]),
     "sihc_gather_cells": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
     "sihc_scatter_cells": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
     "sihc_scatter_add_cells": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
+    "sihc_stream": (_i32, [_vpp, _i32, _vpp, _i32, _sz, _i32, _vp]),
     "sihc_copy": (_i32, [_vp, _vp, _sz, _vp]),
 }
 

@@ -122,6 +122,36 @@ def test_scatter_add_cells_arguments_are_validated():
     assert lib.sihc_scatter_add_cells(None, None, None, 0, 16, 2, 64, _lib.DTYPE_BF16, None) == 0
 
 
+def test_deferred_finalize_arguments_are_validated():
+    lib = _lib.lib()
+    info = (ctypes.c_int * 2)(7, 3)
+    one = _lib.ptr_array([FAKE])
+    nul = _lib.ptr_array([None])
+    rc = lib.sihc_event_backward_partial(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                         2, 16, 2, 64, None, 1, 1, FAKE, 1 << 30, None, None)
+    assert rc == 1 and b"null info" in lib.sihc_last_error()
+    assert lib.sihc_event_finalize(1, one, info, nul, one, 2, 64, 1, None) == 1
+    assert b"null gradient of event 0" in lib.sihc_last_error()
+    bad = (ctypes.c_int * 2)(7, 4)
+    assert lib.sihc_event_finalize(1, one, bad, one, one, 2, 64, 1, None) == 1
+    assert b"bad info" in lib.sihc_last_error()
+    assert lib.sihc_event_finalize(1, one, info, one, one, 3, 64, 1, None) == 1
+    assert lib.sihc_event_finalize(0, None, None, None, None, 2, 64, 1, None) == 0  # nothing to do
+    empty = (ctypes.c_int * 2)(0, 0)  # a zero-token event: no partial rows, nothing read
+    assert lib.sihc_event_finalize(1, nul, empty, nul, nul, 2, 64, 1, None) == 0
+
+
+def test_stream_calibration_arguments_are_validated():
+    lib = _lib.lib()
+    arr = _lib.ptr_array([FAKE, FAKE])
+    assert lib.sihc_stream(arr, 3, arr, 1, 1 << 20, 1024, None) == 1
+    assert b"unsupported mix" in lib.sihc_last_error()
+    assert lib.sihc_stream(arr, 1, arr, 1, 1000, 1024, None) == 1
+    assert b"multiple of 16" in lib.sihc_last_error()
+    assert lib.sihc_stream(_lib.ptr_array([FAKE + 8]), 1, arr, 1, 1 << 20, 1024, None) == 1
+    assert b"misaligned" in lib.sihc_last_error()
+
+
 def test_oversized_tensor_is_rejected():
     lib = _lib.lib()
     outs = _lib.ptr_array([FAKE])

@@ -112,3 +112,33 @@ def test_sixteen_slot_cells_at_batch_32():
     wg = launch.weight_grad(x, ups, a)
     exp = O.weight_grad(x[:, :, :, :32].cpu(), [u[:, :, :32].cpu() for u in ups], 16)
     assert_parity(wg[:, :32], exp.to(bf), bf, what="p4 weight grad (channel slice)", kind="reduced")
+
+
+@pytest.mark.parametrize("nr,nw", [(0, 1), (1, 1), (2, 1), (2, 2), (4, 2)])
+def test_stream_calibration_kernel(nr, nw):
+    # sihc_stream (the HBM ceiling the bench reports): dst_j = XOR of the sources ^ j, and
+    # the write-only mix stores the 16-byte vector index pattern
+    import ctypes
+
+    from sihc_hip import _lib
+
+    announce(f"stream calibration {nr}:{nw}")
+    L = _lib.lib()
+    n = (1 << 20) + 16 * 7  # bytes: not a multiple of the grid's stride
+    g = torch.Generator(device="cuda").manual_seed(nr * 10 + nw)
+    srcs = [torch.randint(0, 2 ** 31 - 1, (n // 4,), device="cuda", generator=g, dtype=torch.int32) for _ in range(nr)]
+    dsts = [torch.zeros(n // 4, device="cuda", dtype=torch.int32) for _ in range(nw)]
+    sp = (ctypes.c_void_p * max(nr, 1))(*[t.data_ptr() for t in srcs])
+    dp = (ctypes.c_void_p * nw)(*[t.data_ptr() for t in dsts])
+    _lib.check(L.sihc_stream(sp, nr, dp, nw, n, 64, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    torch.cuda.synchronize()
+    if nr:
+        acc = srcs[0].clone()
+        for t in srcs[1:]:
+            acc ^= t
+    else:
+        idx = torch.arange(n // 16, device="cuda", dtype=torch.int64)
+        acc = torch.stack([idx & 0xFFFFFFFF, idx >> 32, torch.zeros_like(idx), torch.zeros_like(idx)], 1)
+        acc = acc.to(torch.int64).view(-1).to(torch.int32)
+    for j, d in enumerate(dsts):
+        assert torch.equal(d, acc ^ j), f"output {j}"

@@ -134,3 +134,53 @@ def test_event_op_handles_unused_outputs():
         assert_parity(a, b, torch.float32)
     gx2, = torch.autograd.grad(x_out.sum(), (x,))
     assert torch.equal(gx2, torch.ones_like(gx2))
+
+
+def test_deferred_finalize_matches_per_call_finalize():
+    # sihc_event_backward_partial over a chain of 35 events (full, write-only and read-only
+    # modes), then one sihc_event_finalize (two launches: 32 + 3 events): every output
+    # bit-identical to sihc_event_backward's own finalize.
+    import ctypes
+
+    from sihc_hip import _lib
+
+    announce("deferred event finalize, 35 events")
+    torch.manual_seed(41)
+    L = _lib.lib()
+    b, c, slots = 3, 136, 4
+    x_out = torch.randn(b, 32, 32, c, device="cuda").to(torch.bfloat16)
+    dz = torch.randn(b, 256, c, device="cuda").to(torch.bfloat16)
+    h = (1e-2 * torch.randn_like(x_out))
+    g = (1e-2 * torch.randn_like(dz))
+    nws = L.sihc_event_backward_workspace_size(b, 16, 2, c)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    n = 35
+    info = (ctypes.c_int * (2 * n))()
+    slot = lambda i: ctypes.cast(ctypes.addressof(info) + 8 * i, ctypes.POINTER(ctypes.c_int))  # noqa: E731
+    works, got, ref = [], [], []
+    for i in range(n):
+        beta = (1.0 + 0.05 * torch.randn(c, slots, device="cuda")).to(torch.bfloat16)
+        alpha = (0.25 + 0.05 * torch.randn(c, slots, device="cuda")).to(torch.bfloat16)
+        mode = ("full", "write", "read")[i % 3]
+        args = dict(full=(h, g, x_out, dz, beta, alpha), write=(h, None, None, dz, beta, None),
+                    read=(h, g, x_out, None, None, alpha))[mode]
+        ref.append(launch.event_backward(*args, carrier_like=x_out))
+        outs = [torch.full_like(t, float("nan")) if t is not None else None for t in ref[-1]]
+        gx = outs[0] if mode != "write" else torch.full_like(x_out, float("nan"))
+        work = torch.empty(nws // 4 + 16, device="cuda", dtype=torch.float32)
+        works.append(work)
+        hh, gz, xo, d, bt, al = args
+        _lib.check(L.sihc_event_backward_partial(p(hh), p(gz), p(xo), p(d), p(bt), p(al), p(gx), p(outs[1]),
+                                                 p(outs[2]), p(outs[3]), b, 16, 2, c, None, 1, 1, p(work),
+                                                 work.numel() * 4, slot(i), st))
+        got.append((gx, *outs[1:]))
+    vp = lambda ts: _lib.ptr_array(None if t is None else t.data_ptr() for t in ts)  # noqa: E731
+    _lib.check(L.sihc_event_finalize(n, vp(works), info, vp([o[2] for o in got]), vp([o[3] for o in got]),
+                                     2, c, 1, st))
+    torch.cuda.synchronize()
+    for i, (a, r) in enumerate(zip(got, ref)):
+        for k in range(4):
+            if r[k] is None:
+                continue
+            assert torch.equal(a[k], r[k]), f"event {i} output {k} differs"
