@@ -175,23 +175,45 @@ class LiteralStep:
                                   self.K, self.C, 1, self.stream)
         return self.L.sihc_event_finalize(*self.finalize_args)
 
-    def run(self, calls, timer=None):
-        """Launch a call list; with `timer` (a dict), HIP events on the launch stream around
-        every full per-event forward and backward launch go to timer[name]."""
-        for name, fn, args, _ in calls:
-            if timer is not None and name in ("event_forward", "event_backward"):
-                start = self.torch.cuda.Event(enable_timing=True)
-                end = self.torch.cuda.Event(enable_timing=True)
-                start.record()
-                self.check(fn(*args))
-                end.record()
-                timer.setdefault(name, []).append((start, end))
-            else:
-                self.check(fn(*args))
+    def run(self, calls):
+        for _, fn, args, _ in calls:
+            self.check(fn(*args))
 
-    def step(self, timer=None):
-        self.run(self.fwd)
-        self.run(self.bwd, timer)
+    def spans(self, calls, name):
+        """(head, body, tail) of a call list: body is the run of consecutive `name` calls
+        (the full per-event launches), head and tail the calls before and after it."""
+        idx = [i for i, c in enumerate(calls) if c[0] == name]
+        lo, hi = idx[0], idx[-1] + 1
+        assert idx == list(range(lo, hi)), f"{name} launches are not consecutive"
+        return calls[:lo], calls[lo:hi], calls[hi:]
+
+    def step(self, marks=None):
+        """One fwd+bwd step. With `marks` (a list), HIP events on the launch stream are
+        recorded only at the ends of the runs of full per-event launches and at the end of
+        the forward, appended as (f0, f1, fe, b0, b1, n_fwd, n_bwd): (f1 - f0) spans the
+        full forward launches, (b1 - b0) the full backward launches, inter-launch gaps
+        included, and fe ends the forward phase. Events between every launch would
+        each add a marker packet and an idle gap of several microseconds to the step."""
+        if marks is None:
+            self.run(self.fwd)
+            self.run(self.bwd)
+            return
+        ev = lambda: self.torch.cuda.Event(enable_timing=True)  # noqa: E731
+        f0, f1, fe, b0, b1 = ev(), ev(), ev(), ev(), ev()
+        fh, fb, ft = self.spans(self.fwd, "event_forward")
+        bh, bb, bt = self.spans(self.bwd, "event_backward")
+        self.run(fh)
+        f0.record()
+        self.run(fb)
+        f1.record()
+        self.run(ft)
+        fe.record()
+        self.run(bh)
+        b0.record()
+        self.run(bb)
+        b1.record()
+        self.run(bt)
+        marks.append((f0, f1, fe, b0, b1, len(fb), len(bb)))
 
 
 def _timed(torch, fn, iters=10, warmup=2):
@@ -821,28 +843,32 @@ def main():
     torch.cuda.synchronize()
     print(f"[bench] warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
 
-    timer: dict = {}
+    # Timed region: the K steps back to back, bracketed by device synchronisation. Inside
+    # each step HIP events mark only the step's phase boundaries and the two runs of full
+    # per-event launches (for the dominant kernels' average launch time).
+    marks: list = []
     t_fwd: list = []
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        a, b, c = ev(), ev(), ev()
+        a, c = ev(), ev()
         a.record()
-        step.run(step.fwd, timer)
-        b.record()
-        step.run(step.bwd, timer)
+        step.step(marks)
         c.record()
-        t_fwd.append((a, b, c))
+        t_fwd.append((a, c))
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = wall / args.steps * 1e3
-    fwd_ms = statistics.median(a.elapsed_time(b) for a, b, _ in t_fwd)
-    bwd_ms = statistics.median(b.elapsed_time(c) for _, b, c in t_fwd)
-    kern_ms = [s.elapsed_time(e) for s, e in timer["event_backward"]]
-    avg_kernel_ms = sum(kern_ms) / len(kern_ms)
-    fwd_kern_ms = [s.elapsed_time(e) for s, e in timer["event_forward"]]
-    avg_fwd_kernel_ms = sum(fwd_kern_ms) / len(fwd_kern_ms)
+    step_ms = statistics.median(a.elapsed_time(c) for a, c in t_fwd)
+    fwd_kern_ms = [f0.elapsed_time(f1) / nf for f0, f1, _, _, _, nf, _ in marks]
+    kern_ms = [b0.elapsed_time(b1) / nb for _, _, _, b0, b1, _, nb in marks]
+    avg_kernel_ms = statistics.median(kern_ms)
+    avg_fwd_kernel_ms = statistics.median(fwd_kern_ms)
+    n_bwd_launches = sum(m[6] for m in marks)
+    # phase split from the step's own events: forward = start .. end of the forward tail
+    fwd_ms = statistics.median(a.elapsed_time(m[2]) for (a, _), m in zip(t_fwd, marks))
+    bwd_ms = statistics.median(m[2].elapsed_time(c) for (_, c), m in zip(t_fwd, marks))
     print(f"[bench] timed {args.steps} steps: {ms_step:.3f} ms/step", file=sys.stderr, flush=True)
 
     total_bytes = step.bytes_fwd + step.bytes_bwd
@@ -892,7 +918,7 @@ def main():
                                "of 1 GiB; not measured in this run") if traffic is not None else None,
             "bytes_per_launch": dom_bytes,
             "avg_launch_ms": round(avg_kernel_ms, 4),
-            "launches": len(kern_ms),
+            "launches": n_bwd_launches,
         },
     }
     if not args.no_extra:
