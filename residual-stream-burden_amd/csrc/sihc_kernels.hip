@@ -61,10 +61,10 @@
 #define SIHC_EV_MINW 1
 #endif
 #ifndef SIHC_EV_CHUNK  // tokens per reduction chunk, per-event backward
-#define SIHC_EV_CHUNK 256
+#define SIHC_EV_CHUNK 128
 #endif
 #ifndef SIHC_EV_MAXCHUNKS  // most reduction chunks (partial rows) of the per-event backward
-#define SIHC_EV_MAXCHUNKS 512
+#define SIHC_EV_MAXCHUNKS 1024
 #endif
 #ifndef SIHC_EV_GROUP  // tokens per interleaved group of a backward chunk (0: contiguous)
 #define SIHC_EV_GROUP 32

@@ -41,7 +41,7 @@ def test_workspace_sizes_are_pure_functions_of_sizes():
     # the query also covers the fused triangular backward: one chunk per 64 tokens, at
     # most 1024 (more than the 152 chunks the 11-update gamma gradient takes)
     assert lib.sihc_triangular_gamma_grad_workspace_size(11, 65536, 1152) == 1024 * 11 * 1152 * 4
-    assert lib.sihc_event_backward_workspace_size(256, 16, 2, 1152) == 256 * 2 * 4 * 1152 * 4
+    assert lib.sihc_event_backward_workspace_size(256, 16, 2, 1152) == 512 * 2 * 4 * 1152 * 4
 
 
 FAKE = 0x1000  # never dereferenced: every call below fails argument validation first

@@ -77,7 +77,7 @@ def test_noalloc_matches_workspace_entry_point_twice(pair):
 
 
 def test_noalloc_rejects_sizes_beyond_its_scratch():
-    # 16 slots, 65,536 tokens, 4096 channels: 256 chunks x 2 x 16 x 4096 x 4 B = 128 MiB of
+    # 16 slots, 65,536 tokens, 4096 channels: 512 chunks x 2 x 16 x 4096 x 4 B = 256 MiB of
     # partial rows, more than the 64 MiB array; rejected from the sizes alone, before any
     # HIP call (so this runs without a GPU)
     L = _lib.lib()
