@@ -61,6 +61,12 @@ def parse_args():
     p.add_argument("--phase", default="train,inference", help="--mode model: train and/or inference")
     p.add_argument("--model-batch", type=int, default=128, help="--mode model: images per step")
     p.add_argument("--no-graph", action="store_true", help="--mode model: inference without HIP-graph capture")
+    p.add_argument("--compile", action="store_true",
+                   help="--mode model: torch.compile the model as the reference's fusion_profile does (train: "
+                        "mode='default', inference: mode='reduce-overhead', dynamic=False)")
+    p.add_argument("--tri-backward", choices=("visible", "fused"), default=None,
+                   help="--mode model --compile: how the triangular op's traced backward returns the update "
+                        "gradients (sihc_hip.sublayer_kernels.COMPILED_TRIANGULAR_BACKWARD)")
     p.add_argument("--mode", choices=("step", "calibrate", "kernels", "e2e", "model"), default="step",
                    help="step: the benchmark (default); calibrate: a 1 GiB copy-kernel launch plus single "
                         "event forward/backward launches at the same shape, for HBM counter runs; kernels: "
@@ -704,14 +710,17 @@ def _torch_controls():
 
 
 def model_step(size: str, implementation: str, phase: str, batch: int, steps: int, warmup: int,
-               graph: bool, seed: int) -> dict:
+               graph: bool, seed: int, compile_model: bool = False) -> dict:
     """One fusion_profile cell on this GPU: the compact SiHC sublayer denoiser of
     sihc_hip.e2e at a reference preset, FP32 parameters under BF16 autocast, batch
     `batch`. train: forward, loss, backward, fused AdamW (lr 2e-4, betas 0.9/0.95) and
     two FP32 EMAs; inference: one forward (HIP-graph captured with `graph`). Routing:
     fused = HIP stage API (reference "fused"), event = HIP per-event schedule,
     factored / literal = the PyTorch controls (reference "factored" / "literal").
-    Bodies run eager (no tracing compiler)."""
+    Bodies run eager unless `compile_model`: then the whole model is compiled as in
+    fusion_profile.py:103 (train mode="default", inference mode="reduce-overhead",
+    dynamic=False; the reference's single-rank DDP wrapper is not reproduced) and the
+    inference step is not captured into a HIP graph by hand."""
     import torch
 
     from sihc_hip.e2e import SiHCDenoiser
@@ -734,7 +743,15 @@ def model_step(size: str, implementation: str, phase: str, batch: int, steps: in
     t = torch.full((batch,), 0.5, device=dev)
     y = torch.arange(batch, device=dev) % 1000
     out = {"size": size, "implementation": implementation, "phase": phase, "batch": batch,
-           "params": sum(p.numel() for p in model.parameters())}
+           "params": sum(p.numel() for p in model.parameters()), "compiled": compile_model}
+    runner = model
+    if compile_model:
+        import torch._inductor.config as inductor_config
+
+        torch._dynamo.config.cache_size_limit = 128
+        inductor_config.compile_threads = min(8, inductor_config.compile_threads)  # bounded worker pool
+        runner = torch.compile(model, mode="default" if phase == "train" else "reduce-overhead", dynamic=False)
+        graph = False
     if phase == "train":
         model.train()
         target = torch.randn(batch, 3, 256, 256, device=dev, generator=g)
@@ -742,10 +759,15 @@ def model_step(size: str, implementation: str, phase: str, batch: int, steps: in
         opt = torch.optim.AdamW(params, lr=2e-4, betas=(0.9, 0.95), weight_decay=0, fused=True)
         emas = [[p.detach().clone() for p in params] for _ in range(2)]
 
-        def run():
+        def run(first=False):
             opt.zero_grad(set_to_none=True)
+            tc = time.perf_counter()
             with torch.autocast("cuda", dtype=torch.bfloat16):
-                loss = (model(x, t, y).float() - target).square().flatten(1).mean(1).mean()
+                loss = (runner(x, t, y).float() - target).square().flatten(1).mean(1).mean()
+            if first:
+                torch.cuda.synchronize()
+                print(f"[bench] {size} {implementation} train: first forward {time.perf_counter() - tc:.1f} s",
+                      file=sys.stderr, flush=True)
             loss.backward()
             opt.step()
             with torch.no_grad():
@@ -774,11 +796,18 @@ def model_step(size: str, implementation: str, phase: str, batch: int, steps: in
                 return result
         else:
             def run():
+                if compile_model:
+                    torch.compiler.cudagraph_mark_step_begin()
                 with torch.inference_mode(), torch.autocast("cuda", dtype=torch.bfloat16):
-                    return model(x, t, y)
+                    return runner(x, t, y)
     last = None
-    for _ in range(warmup):
-        last = run()
+    tc = time.perf_counter()
+    for i in range(warmup):
+        last = run(first=True) if i == 0 and phase == "train" and compile_model else run()
+        if i == 0 and compile_model:
+            torch.cuda.synchronize()
+            print(f"[bench] {size} {implementation} {phase}: first (compiling) step {time.perf_counter() - tc:.1f} s",
+                  file=sys.stderr, flush=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -793,13 +822,19 @@ def model_step(size: str, implementation: str, phase: str, batch: int, steps: in
 
 
 def model_bench(args) -> None:
+    if args.tri_backward:
+        from sihc_hip import sublayer_kernels
+
+        sublayer_kernels.COMPILED_TRIANGULAR_BACKWARD = args.tri_backward
     for size in args.size.split(","):
         for phase in args.phase.split(","):
             for impl in args.implementation.split(","):
                 import torch
                 try:
                     r = model_step(size, impl, phase, args.model_batch, args.steps, args.warmup,
-                                   not args.no_graph, args.seed)
+                                   not args.no_graph, args.seed, args.compile)
+                    if args.compile and args.tri_backward:
+                        r["tri_backward"] = args.tri_backward
                 except torch.OutOfMemoryError:
                     r = {"size": size, "implementation": impl, "phase": phase, "status": "oom"}
                 print(json.dumps(r), flush=True)

@@ -182,11 +182,34 @@ def _tri_setup(ctx, inputs, output):
     ctx.save_for_backward(gamma, *updates)
 
 
+# How the triangular op's backward hands out the update gradients grad * gamma_j when
+# torch.compile traces it (eager calls always take the one-pass HIP op):
+#   "visible": the reference's fp32 products cast to the workspace dtype as plain torch
+#              ops (:373-378), which Inductor fuses with the gradient accumulation of each
+#              update, plus the gamma reduction op (:355-361);
+#   "fused":   the one-pass HIP op, whose [A, B, N, C] stack of update gradients is
+#              materialised before the accumulation.
+COMPILED_TRIANGULAR_BACKWARD = "visible"
+
+
+def _traced() -> bool:
+    """True while torch.compile (AOTAutograd) traces an autograd rule. The public
+    torch.compiler.is_compiling() is False there; an active tracing context is not."""
+    return torch._guards.TracingContext.try_get() is not None
+
+
 def _tri_autograd(ctx, grad):
     """Reference :369-379: identity to base, grad * gamma_j to each active update and
-    the gamma reduction, all from `_tri_backward`."""
+    the gamma reduction. Eager: all from one pass over grad (`_tri_backward`); under
+    torch.compile the products stay visible to the compiler unless
+    COMPILED_TRIANGULAR_BACKWARD is "fused"."""
     gamma, *updates = ctx.saved_tensors
-    ddz, dg = _tri_backward(grad.contiguous(), updates, gamma)
+    grad = grad.contiguous()
+    if COMPILED_TRIANGULAR_BACKWARD == "visible" and _traced():
+        g32 = grad.float()
+        ddz = [(g32 * gamma[j].float()).to(grad.dtype) for j in range(len(updates))]
+        return grad, ddz, _tri_gamma_backward(grad, updates, gamma)
+    ddz, dg = _tri_backward(grad, updates, gamma)
     return grad, list(ddz.unbind(0)), dg
 
 
@@ -239,5 +262,5 @@ def _tri_backward_fake(grad, updates, gamma):
     return grad.new_empty((len(updates), *grad.shape)), torch.empty_like(gamma)
 
 
-__all__ = ["sublayer_read", "sublayer_write", "sublayer_triangular", "_write_impl",
+__all__ = ["sublayer_read", "sublayer_write", "sublayer_triangular", "_write_impl", "COMPILED_TRIANGULAR_BACKWARD",
            "_weights_backward", "_tri_gamma_backward", "_tri_backward", "_require_packed", "_geometry"]
