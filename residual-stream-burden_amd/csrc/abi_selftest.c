@@ -3,9 +3,12 @@
  *
  * Shows that the library needs nothing but the HIP runtime and this header: it
  * allocates device buffers, calls read / write / weight gradient / triangular /
- * fused triangular backward on small fp32 shapes, and checks every result against
- * direct loops over the cell index map (token m = b*G*G + wy*G + wx, slot
- * s = uy*K + ux -> carrier pixel (b, wy*K + uy, wx*K + ux)), plus one argument error.
+ * fused triangular backward, the per-event fused forward and backward (with and
+ * without a state index) and the cell gather / scatter on small fp32 shapes, and
+ * checks every result against direct loops over the cell index map (token
+ * m = b*G*G + n reads cell n, or cell index[m] with a state index; cell n = wy*G + wx,
+ * slot s = uy*K + ux -> carrier pixel (b, wy*K + uy, wx*K + ux)), plus one argument
+ * error.
  * Exit status 0 when every check passes. Built next to libsihc_hip.so by build.py.
  */
 #include <hip/hip_runtime_api.h>
@@ -20,6 +23,7 @@ enum { B = 2, G = 4, K = 2, S = K * K, C = 24, E = 3, M = B * G * G, GK = G * K 
 #define NX (B * GK * GK * C)
 #define NZ (M * C)
 
+static int failures;
 static unsigned long long rng_state = 12345u;
 static float rnd(void) { /* uniform in [-1, 1) from a 64-bit LCG */
   rng_state = rng_state * 6364136223846793005ull + 1442695040888963407ull;
@@ -32,7 +36,20 @@ static long xoff(int m, int s, int c) {
   return ((long)(b * GK + row) * GK + col) * C + c;
 }
 
-static int failures = 0;
+/* the same with a state index: token m reads cell index[m] of its batch image */
+static long xoff_idx(const int32_t *index, int m, int s, int c) {
+  if (!index) return xoff(m, s, c);
+  const int b = m / (G * G);
+  return xoff(b * G * G + index[m], s, c);
+}
+
+static int bit_equal(const char *what, const float *got, const float *want, int n) {
+  const int ok = memcmp(got, want, (size_t)n * sizeof(float)) == 0;
+  printf("%-28s %s\n", what, ok ? "bit-exact ok" : "FAIL (bits differ)");
+  if (!ok) ++failures;
+  return ok;
+}
+
 static void check(const char *what, const float *got, const double *want, int n, double tol) {
   double worst = 0.0, scale = 0.0;
   for (int i = 0; i < n; ++i) {
@@ -176,6 +193,117 @@ int main(void) {
         want[j * C + c] = a;
       }
     check("triangular backward dgamma", got, want, 2 * C, 1e-5);
+  }
+
+  /* per-event fused forward and backward, without and with a permutation state index */
+  {
+    static int32_t idx[M];
+    for (int m = 0; m < M; ++m) idx[m] = (m % (G * G) * 7 + 3) % (G * G); /* 7 is coprime to G*G */
+    int32_t *didx;
+    HIP_OK(hipMalloc((void **)&didx, sizeof idx));
+    HIP_OK(hipMemcpy(didx, idx, sizeof idx, hipMemcpyHostToDevice));
+    static float xo[NX], gxo[NX], gx[NX], zo[NZ], gzo[NZ], gdz[NZ], gb[C * S], ga[C * S];
+    static double want_b[C * S], want_a[C * S];
+    for (int i = 0; i < NX; ++i) gxo[i] = 0.1f * rnd();
+    for (int i = 0; i < NZ; ++i) gzo[i] = 0.1f * rnd();
+    float *dxo, *dgxo, *dgx, *dzo, *dgzo, *dgdz, *dgb, *dga;
+    void *ework;
+    const size_t ebytes = sihc_event_backward_workspace_size(B, G, K, C);
+    HIP_OK(hipMalloc((void **)&dxo, sizeof xo));
+    HIP_OK(hipMalloc((void **)&dgxo, sizeof gxo));
+    HIP_OK(hipMalloc((void **)&dgx, sizeof gx));
+    HIP_OK(hipMalloc((void **)&dzo, sizeof zo));
+    HIP_OK(hipMalloc((void **)&dgzo, sizeof gzo));
+    HIP_OK(hipMalloc((void **)&dgdz, sizeof gdz));
+    HIP_OK(hipMalloc((void **)&dgb, sizeof gb));
+    HIP_OK(hipMalloc((void **)&dga, sizeof ga));
+    HIP_OK(hipMalloc(&ework, ebytes));
+    HIP_OK(hipMemcpy(dgxo, gxo, sizeof gxo, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dgzo, gzo, sizeof gzo, hipMemcpyHostToDevice));
+    const float *be = beta, *an = alpha + C * S; /* event 0's write, event 1's read */
+    for (int use_idx = 0; use_idx < 2; ++use_idx) {
+      const int32_t *hidx = use_idx ? idx : NULL;
+      char name[64];
+      /* forward: x_out = x + beta (.) dz at the token's cell, z_out = sum_s alpha' x_out */
+      SIHC_OK_(sihc_event_forward(dx, dz[0], dbeta, dalpha + C * S, dxo, dzo, B, G, K, C, use_idx ? didx : NULL,
+                                  SIHC_DTYPE_F32, NULL));
+      HIP_OK(hipMemcpy(xo, dxo, sizeof xo, hipMemcpyDeviceToHost));
+      HIP_OK(hipMemcpy(zo, dzo, sizeof zo, hipMemcpyDeviceToHost));
+      for (int m = 0; m < M; ++m)
+        for (int c = 0; c < C; ++c) {
+          double a = 0.0;
+          for (int s2 = 0; s2 < S; ++s2) {
+            const long o = xoff_idx(hidx, m, s2, c);
+            const float w = (float)((double)x[o] + (double)be[c * S + s2] * z[0][m * C + c]);
+            want_x[o] = w;
+            a += (double)an[c * S + s2] * w;
+          }
+          want_z[m * C + c] = a;
+        }
+      snprintf(name, sizeof name, "event forward x_out%s", use_idx ? " (index)" : "");
+      check(name, xo, want_x, NX, 1e-6);
+      snprintf(name, sizeof name, "event forward z_out%s", use_idx ? " (index)" : "");
+      check(name, zo, want_z, NZ, 1e-5);
+      /* backward: t = gxo + alpha' gzo; gx = t; gdz = sum_s beta t; gbeta = sum_m dz t;
+         galpha' = sum_m x_out gzo */
+      SIHC_OK_(sihc_event_backward(dgxo, dgzo, dxo, dz[0], dbeta, dalpha + C * S, dgx, dgdz, dgb, dga, B, G, K, C,
+                                   use_idx ? didx : NULL, SIHC_DTYPE_F32, SIHC_DTYPE_F32, ework, ebytes, NULL));
+      HIP_OK(hipMemcpy(gx, dgx, sizeof gx, hipMemcpyDeviceToHost));
+      HIP_OK(hipMemcpy(gdz, dgdz, sizeof gdz, hipMemcpyDeviceToHost));
+      HIP_OK(hipMemcpy(gb, dgb, sizeof gb, hipMemcpyDeviceToHost));
+      HIP_OK(hipMemcpy(ga, dga, sizeof ga, hipMemcpyDeviceToHost));
+      for (int i = 0; i < C * S; ++i) want_b[i] = want_a[i] = 0.0;
+      for (int m = 0; m < M; ++m)
+        for (int c = 0; c < C; ++c) {
+          double d = 0.0;
+          for (int s2 = 0; s2 < S; ++s2) {
+            const long o = xoff_idx(hidx, m, s2, c);
+            const double t = (double)gxo[o] + (double)an[c * S + s2] * gzo[m * C + c];
+            want_x[o] = t;
+            d += (double)be[c * S + s2] * t;
+            want_b[c * S + s2] += (double)z[0][m * C + c] * t;
+            want_a[c * S + s2] += (double)xo[o] * gzo[m * C + c];
+          }
+          want_z[m * C + c] = d;
+        }
+      snprintf(name, sizeof name, "event backward dX%s", use_idx ? " (index)" : "");
+      check(name, gx, want_x, NX, 1e-6);
+      snprintf(name, sizeof name, "event backward ddz%s", use_idx ? " (index)" : "");
+      check(name, gdz, want_z, NZ, 1e-5);
+      snprintf(name, sizeof name, "event backward dbeta%s", use_idx ? " (index)" : "");
+      check(name, gb, want_b, C * S, 1e-5);
+      snprintf(name, sizeof name, "event backward dalpha'%s", use_idx ? " (index)" : "");
+      check(name, ga, want_a, C * S, 1e-5);
+    }
+
+    /* gather / scatter of whole cells: bit-exact copies; scatter(gather(x)) == x */
+    {
+      static float cells[M * S * C], want_cells[M * S * C], back[NX];
+      float *dcells, *dback;
+      HIP_OK(hipMalloc((void **)&dcells, sizeof cells));
+      HIP_OK(hipMalloc((void **)&dback, sizeof back));
+      SIHC_OK_(sihc_gather_cells(dx, didx, dcells, B, G, K, C, SIHC_DTYPE_F32, NULL));
+      HIP_OK(hipMemcpy(cells, dcells, sizeof cells, hipMemcpyDeviceToHost));
+      for (int m = 0; m < M; ++m)
+        for (int s2 = 0; s2 < S; ++s2)
+          for (int c = 0; c < C; ++c) want_cells[((long)m * S + s2) * C + c] = x[xoff_idx(idx, m, s2, c)];
+      bit_equal("gather cells (index)", cells, want_cells, M * S * C);
+      SIHC_OK_(sihc_scatter_cells(dcells, didx, dback, B, G, K, C, SIHC_DTYPE_F32, NULL));
+      HIP_OK(hipMemcpy(back, dback, sizeof back, hipMemcpyDeviceToHost));
+      bit_equal("scatter(gather(x)) == x", back, x, NX);
+      (void)hipFree(dcells);
+      (void)hipFree(dback);
+    }
+    (void)hipFree(didx);
+    (void)hipFree(dxo);
+    (void)hipFree(dgxo);
+    (void)hipFree(dgx);
+    (void)hipFree(dzo);
+    (void)hipFree(dgzo);
+    (void)hipFree(dgdz);
+    (void)hipFree(dgb);
+    (void)hipFree(dga);
+    (void)hipFree(ework);
   }
 
   /* argument errors are reported before any launch */

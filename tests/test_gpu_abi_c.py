@@ -2,9 +2,12 @@
 
 `sihc_abi_selftest` (residual-stream-burden_amd/csrc/abi_selftest.c, built next to
 libsihc_hip.so by build.py) allocates device memory through the HIP runtime, calls
-read / write / weight gradient / triangular / fused triangular backward through
-include/sihc_hip.h on fp32 inputs, compares every result with direct loops over the
-cell index map, and checks that an argument error is reported before any launch.
+read / write / weight gradient / triangular / fused triangular backward, the per-event
+fused forward and backward (without and with a permutation state index) and the cell
+gather / scatter through include/sihc_hip.h on fp32 inputs, compares every result with
+direct loops over the cell index map (the cell copies bit for bit, including
+scatter(gather(x)) == x), and checks that an argument error is reported before any
+launch.
 """
 from __future__ import annotations
 
