@@ -63,16 +63,18 @@ def parse_args():
     p.add_argument("--no-graph", action="store_true", help="--mode model: inference without HIP-graph capture")
     p.add_argument("--compile", action="store_true",
                    help="--mode model: torch.compile the model as the reference's fusion_profile does (train: "
-                        "mode='default', inference: mode='reduce-overhead', dynamic=False)")
+                        "mode='default', inference: mode='reduce-overhead', dynamic=False); --mode stage: compile "
+                        "the stage schedule's forward (fullgraph) and run the compiled backward")
     p.add_argument("--tri-backward", choices=("visible", "fused"), default=None,
                    help="--mode model --compile: how the triangular op's traced backward returns the update "
                         "gradients (sihc_hip.sublayer_kernels.COMPILED_TRIANGULAR_BACKWARD)")
-    p.add_argument("--mode", choices=("step", "calibrate", "kernels", "e2e", "model"), default="step",
+    p.add_argument("--mode", choices=("step", "calibrate", "kernels", "e2e", "model", "stage"), default="step",
                    help="step: the benchmark (default); calibrate: a 1 GiB copy-kernel launch plus single "
                         "event forward/backward launches at the same shape, for HBM counter runs; kernels: "
                         "every HIP kernel timed alone at the benchmark shape (one JSON line per kernel); e2e: "
                         "benchmark config 4, a SiHC-XL denoiser forward on a CFG batch with HIP routing; model: the "
-                        "reference's fusion_profile matrix (presets x routing implementation x train/inference)")
+                        "reference's fusion_profile matrix (presets x routing implementation x train/inference); "
+                        "stage: benchmark config 2 on the reference's stage API (the drop-in path) only")
     return p.parse_args()
 
 
@@ -394,7 +396,7 @@ def extra_configs(seed: int) -> dict:
     return out
 
 
-def stage_api_config2(seed: int, steps: int = 3) -> dict:
+def stage_api_config2(seed: int, steps: int = 3, compiled: bool = False) -> dict:
     """Benchmark config 2 on the reference's own schedule (sublayer.py:52-72), the drop-in
     path: per stage of 8/12/8 blocks (16/24/16 events) read -> triangular -> write through
     the sihc:: custom ops, then torch autograd back through them, batch 256, D = 1152, bf16.
@@ -403,7 +405,13 @@ def stage_api_config2(seed: int, steps: int = 3) -> dict:
     gradients of the read outputs z_i. Bytes: the algorithmic bytes of the kernel ops
     launched (read (S+E), triangular i (i+2), write (2S+E); backward: update reads and the
     weight gradients (S+E) each, fused triangular backward (1+2i)); the time also covers
-    autograd's own work (gamma products, gradient accumulation in bf16)."""
+    autograd's own work. Eagerly, autograd adds up each update's gradient contributions
+    (one from the write's adjoint, one from every later triangular op of its stage) in
+    bf16, E(E-1)/2 adds of 3 U per stage: that traffic is reported apart
+    (accumulation_units) and in the all-traffic rate. With `compiled`, the schedule's
+    forward is compiled by Inductor (mode="default", fullgraph) and autograd runs the
+    compiled backward, where the triangular update gradients stay visible to Inductor and
+    are fused with that accumulation."""
     import torch
 
     from sihc_hip.sublayer_kernels import sublayer_read, sublayer_triangular, sublayer_write
@@ -422,23 +430,35 @@ def stage_api_config2(seed: int, steps: int = 3) -> dict:
     gzs = [[r((B, 256, C), 0.0, 1e-2) for _ in range(e)] for e in stages]
     g_out = r((B, 32, 32, C), 0.0, 1e-2)
 
-    def run():
-        x = x0
-        outs, grads = [], []
-        for alpha, beta, dz, gz in zip(alphas, betas, dzs, gzs):
+    def forward(x, alphas, betas, dzs):
+        outs = []
+        for alpha, beta, dz in zip(alphas, betas, dzs):
             base = sublayer_read(x, alpha)
             gamma = (alpha[:, None] * beta[None, :]).sum(-1)
             for i in range(len(dz)):
-                z = base[i] if i == 0 else sublayer_triangular(base[i], dz[:i], gamma[i, :i].contiguous())
-                outs.append(z)
-                grads.append(gz[i])
+                outs.append(base[i] if i == 0 else sublayer_triangular(base[i], dz[:i], gamma[i, :i].contiguous()))
             x = sublayer_write(x, dz, beta)
-        torch.autograd.backward(outs + [x], grads + [g_out])
+        return outs, x
+
+    fwd = forward
+    if compiled:
+        torch._dynamo.reset()
+        fwd = torch.compile(forward, mode="default", fullgraph=True)
+    flat_gz = [g for gs in gzs for g in gs]
+
+    def run():
+        outs, x = fwd(x0, alphas, betas, dzs)
+        torch.autograd.backward(outs + [x], flat_gz + [g_out])
 
     fwd_u = sum((S + e) + sum(i + 2 for i in range(1, e)) + (2 * S + e) for e in stages)
     bwd_u = sum(4 * (S + e) + sum(1 + 2 * i for i in range(1, e)) for e in stages)
+    acc_u = sum(3 * e * (e - 1) // 2 for e in stages)  # eager autograd: bf16 a + b per extra contribution
+    tc = time.perf_counter()
     for _ in range(1):
         run()
+    if compiled:
+        torch.cuda.synchronize()
+        print(f"[bench] stage API compiled: first step {time.perf_counter() - tc:.1f} s", file=sys.stderr, flush=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -449,10 +469,22 @@ def stage_api_config2(seed: int, steps: int = 3) -> dict:
     sec = (time.perf_counter() - t0) / steps
     nbytes = (fwd_u + bwd_u) * U
     out = {"workload": "benchmark config 2 on the reference's stage schedule (read -> triangular -> write, stages "
-                       "8/12/8) through the sihc:: custom ops, fwd + autograd bwd, batch 256, D=1152, bf16",
+                       "8/12/8) through the sihc:: custom ops, fwd + autograd bwd, batch 256, D=1152, bf16"
+                       + (", forward compiled by Inductor (fullgraph), compiled backward" if compiled else ", eager"),
            "ms_per_step": round(sec * 1e3, 3), "kernel_op_bytes": nbytes, "fwd_units": fwd_u, "bwd_units": bwd_u,
            "GB/s": round(nbytes / sec / 1e9, 1), "frac_of_peak": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
            "tokens_per_s": round(B * 256 / sec, 1)}
+    if compiled:
+        # traffic of the compiled backward: the gamma reduction (1 + i) U per triangular op
+        # instead of the fused (1 + 2i) U, and one fused pass per update gradient (the later
+        # read gradients, the write adjoint's contribution and the result: E - 1 - j + 2)
+        cb = sum(4 * (S + e) + sum(1 + i for i in range(1, e)) + sum(e - 1 - j + 2 for j in range(e)) for e in stages)
+        out.update({"compiled_bwd_units": cb, "compiled_traffic_GB/s": round((fwd_u + cb) * U / sec / 1e9, 1)})
+    else:
+        allb = nbytes + acc_u * U
+        out.update({"accumulation_units": acc_u, "all_traffic_bytes": allb,
+                    "all_traffic_GB/s": round(allb / sec / 1e9, 1),
+                    "all_traffic_frac_of_peak": round(allb / sec / 1e9 / HBM_PEAK_GBS, 4)})
     del x0, alphas, betas, dzs, gzs, g_out
     torch.cuda.empty_cache()
     return out
@@ -869,6 +901,9 @@ def main():
     if args.mode == "model":
         model_bench(args)
         return
+    if args.mode == "stage":
+        print(json.dumps(stage_api_config2(args.seed, max(1, args.steps), args.compile)), flush=True)
+        return
     print(f"[bench] building step: batch={args.batch} C={args.channels} events={args.events}", file=sys.stderr,
           flush=True)
     step = LiteralStep(args.batch, args.channels, args.events, args.seed)
@@ -961,8 +996,12 @@ def main():
         torch.cuda.empty_cache()
         print("[bench] secondary configs 1 and 3", file=sys.stderr, flush=True)
         result["extra"] = extra_configs(args.seed)
-        print("[bench] config 2 on the stage API (drop-in path)", file=sys.stderr, flush=True)
+        print("[bench] config 2 on the stage API (drop-in path), eager and compiled", file=sys.stderr, flush=True)
         result["extra"]["config2_stage_api"] = stage_api_config2(args.seed)
+        try:
+            result["extra"]["config2_stage_api_compiled"] = stage_api_config2(args.seed, compiled=True)
+        except Exception as exc:  # the headline line must not depend on the compiler
+            result["extra"]["config2_stage_api_compiled"] = {"error": f"{type(exc).__name__}: {exc}"[:300]}
         result["extra"]["stream_ceiling"] = ceiling = stream_ceiling()
         fw_rate = result["fwd_kernel_GBps"]
         result["extra"]["fraction_of_stream_ceiling"] = {
