@@ -134,6 +134,9 @@
 #ifndef SIHC_WG_PAD  // most idle event lanes added to make k_wgrad blocks 4 whole waves
 #define SIHC_WG_PAD 4
 #endif
+#ifndef SIHC_TRIB_WAVES  // fused triangular backward: k_trib_waves from this many updates (0: never)
+#define SIHC_TRIB_WAVES 4
+#endif
 #ifndef SIHC_TRIB_CHUNK  // tokens per reduction chunk, fused triangular backward
 #define SIHC_TRIB_CHUNK 64
 #endif
@@ -826,6 +829,160 @@ __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack 
   for (int ss = 0; ss < S; ++ss) {
 #pragma unroll
     for (int v = 0; v < V; ++v) prow[int64_t(ss) * g.C + c0 + v] = acc[ss][v];
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// Fused triangular backward for many updates (workspace mode, whole 16-byte vectors):
+//   d_e[m,c] = grad[m,c] * gamma[e,c]    part[chunk][e][c] = sum_{m in chunk} grad * z_e
+// One block per (channel slice of 16 lanes x V channels, token chunk). The block stages
+// a sub-tile of up to TRIB_TT gradient rows, and the slice of gamma, in LDS as fp32 once;
+// then each of its waves takes the updates w, w + NW, ... in turn and streams ONE update
+// in and ONE update gradient out at a time. A wave whose loads and stores spread over
+// many arrays at once streams markedly slower (a flat 1:1 copy over 24 + 24 arrays:
+// 5.3 TB/s when every thread touches all of them, 5.7 when each block touches one; 6.5
+// with one array each way), which is what the event-lane kernel k_wgrad does. Each
+// lane owns V channels of 4 token rows (16 lanes x 4 rows per wave); the rows of one
+// update are loaded as raw words, all before the first use. The 4 rows of a wave are
+// added with two fixed-order lane exchanges, so the partial rows are deterministic. ONE:
+// the chunk is a single sub-tile (the usual case), so each update's accumulators live
+// only while the wave streams it; otherwise they stay in registers across sub-tiles.
+// ----------------------------------------------------------------------------------
+#define TRIB_TT 64        // most gradient rows per staged sub-tile
+#define TRIB_MAXK 8       // most updates per wave (E <= TRIB_MAXK * waves)
+#ifndef SIHC_TRIB_RB      // rows of one update loaded per batch by a lane (of TRIB_TT / 4)
+#define SIHC_TRIB_RB 8
+#endif
+#ifndef SIHC_TRIB_MINB    // occupancy hint of k_trib_waves (blocks per CU)
+#define SIHC_TRIB_MINB 1
+#endif
+template <typename T, int V, bool ONE>
+__global__ void __launch_bounds__(256, SIHC_TRIB_MINB) k_trib_waves(const T* __restrict__ grad, PtrPack z, float* __restrict__ part,
+                                                    int E, Geo g, int tpb, int nslices, PtrPack dout,
+                                                    const void* __restrict__ gam, int gam_f32) {
+  constexpr int LX = 16, RY = 4, BC = LX * V, RPL = TRIB_TT / RY;  // rows per lane per sub-tile
+  constexpr bool NTL = true, NTS = true;
+  extern __shared__ float lds[];
+  float* gt = lds;                 // [TRIB_TT][BC] gradient rows
+  float* gm = lds + TRIB_TT * BC;  // [E][BC] gamma slice
+  const int NW = int(blockDim.x) / 64;
+  const int blk = int(blockIdx.x), slice = blk % nslices, chunk = blk / nslices;
+  const int cs = slice * BC;
+  const int tid = int(threadIdx.x), wave = tid / 64, lane = tid % 64;
+  const int lx = lane % LX, ly = lane / LX;
+  const int c0 = cs + lx * V;
+  const bool cok = c0 < g.C;  // the host guarantees C % V == 0: a lane is all in or all out
+  const int m_begin = chunk * tpb;
+  const int m_end = min(m_begin + tpb, g.M);
+  // gamma slice, once per block
+  for (int i = tid; i < E * BC; i += blockDim.x) {
+    const int e = i / BC, c = cs + (i - e * BC);
+    const int64_t gi = int64_t(e) * g.C + min(c, g.C - 1);
+    gm[i] = gam_f32 ? static_cast<const float*>(gam)[gi] : to_f32(static_cast<const bf16_t*>(gam)[gi]);
+  }
+  constexpr int NK = ONE ? 1 : TRIB_MAXK;  // accumulator sets held across sub-tiles
+  float acc[NK][V];
+#pragma unroll
+  for (int k = 0; k < NK; ++k)
+#pragma unroll
+    for (int v = 0; v < V; ++v) acc[k][v] = 0.f;
+  // the 4 token rows of a wave (lanes lx, lx + 16, lx + 32, lx + 48) in fixed order, then
+  // the partial row of update e
+  auto emit = [&](float (&a)[V], int e) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      float t = a[v];
+      t += __shfl_xor(t, 16);
+      t += __shfl_xor(t, 32);
+      a[v] = t;
+    }
+    if (ly == 0 && cok) {
+      float* prow = part + (int64_t(chunk) * E + e) * g.C + c0;
+#pragma unroll
+      for (int v = 0; v < V; ++v) prow[v] = a[v];
+    }
+  };
+  for (int s0 = m_begin; s0 < m_end; s0 += TRIB_TT) {
+    const int tn = min(TRIB_TT, m_end - s0);
+    // stage the gradient rows of this sub-tile (4 vectors per thread in flight)
+    for (int i0 = tid; i0 < tn * LX; i0 += 4 * int(blockDim.x)) {
+      float gv[4][V];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int i = min(i0 + q * int(blockDim.x), tn * LX - 1);
+        const int row = i / LX, c = cs + (i - row * LX) * V;
+        if (c < g.C) {
+          load_vec<T, V, NTL>(grad + int64_t(s0 + row) * g.C + c, gv[q]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < V; ++v) gv[q][v] = 0.f;
+        }
+      }
+      load_fence();
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int i = i0 + q * int(blockDim.x);
+        if (i < tn * LX) {
+#pragma unroll
+          for (int v = 0; v < V; ++v) gt[i * V + v] = gv[q][v];  // row-major [row][BC]
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < TRIB_MAXK; ++k) {
+      const int e = wave + k * NW;
+      float (&ak)[V] = acc[ONE ? 0 : k];
+      if (e < E && cok) {
+        const T* __restrict__ ze = static_cast<const T*>(z.p[e]);
+        T* __restrict__ de = static_cast<T*>(const_cast<void*>(dout.p[e]));
+        float gmv[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) gmv[v] = gm[e * BC + lx * V + v];
+        constexpr int RB = SIHC_TRIB_RB < RPL ? SIHC_TRIB_RB : RPL;
+#pragma unroll
+        for (int r0 = 0; r0 < RPL; r0 += RB) {
+        RawVec<T, V> zr[RB];
+#pragma unroll
+        for (int rr = 0; rr < RB; ++rr) {
+          const int t = min(ly + (r0 + rr) * RY, tn - 1);  // past the sub-tile: a repeated row, loaded not used
+          load_raw<T, V, NTL>(ze + int64_t(s0 + t) * g.C + c0, zr[rr]);
+        }
+        load_fence();
+#pragma unroll
+        for (int rr = 0; rr < RB; ++rr) {
+          const int r = r0 + rr;
+          const int t = ly + r * RY;
+          if (t < tn) {
+            float zv[V], d[V];
+            raw_to_f32<T, V>(zr[rr], zv);
+            const float* gr = gt + t * BC + lx * V;
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+              ak[v] = fmaf(gr[v], zv[v], ak[v]);
+              d[v] = gr[v] * gmv[v];
+            }
+            store_vec<T, V, NTS>(de + int64_t(s0 + t) * g.C + c0, d);
+          }
+        }
+        }
+      }
+      if constexpr (ONE) {  // wave-uniform: every lane exchanges
+        if (e < E) {
+          emit(ak, e);
+#pragma unroll
+          for (int v = 0; v < V; ++v) ak[v] = 0.f;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if constexpr (!ONE) {
+#pragma unroll
+    for (int k = 0; k < TRIB_MAXK; ++k) {
+      const int e = wave + k * NW;
+      if (e < E) emit(acc[k], e);
+    }
   }
 }
 
@@ -2124,9 +2281,25 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
                 direct(IC<1>{});
               }
             } else {
-              hipLaunchKernelGGL((k_wgrad<T, VV, KK, CAR, SD>), dim3(blocks1d(slices, chunks)), dim3(bcg, lanes),
-                                 lds, st, static_cast<const T*>(x), pk, part, index, events, g, tpb, slices, tt, dk,
-                                 gamma, gf32);
+              bool waves = false;
+              if constexpr (SD && VV * sizeof(T) == 16) {
+                // many updates: each wave streams one update at a time (k_trib_waves)
+                waves = SIHC_TRIB_WAVES > 0 && events >= SIHC_TRIB_WAVES && g.C % VV == 0;
+                if (waves) {
+                  const int slicesw = (g.C + 16 * VV - 1) / (16 * VV);
+                  const size_t ldsw = size_t(TRIB_TT + events) * 16 * VV * sizeof(float);
+                  if (tpb <= TRIB_TT)
+                    hipLaunchKernelGGL((k_trib_waves<T, VV, true>), dim3(blocks1d(slicesw, chunks)), dim3(256), ldsw,
+                                       st, static_cast<const T*>(x), pk, part, events, g, tpb, slicesw, dk, gamma, gf32);
+                  else
+                    hipLaunchKernelGGL((k_trib_waves<T, VV, false>), dim3(blocks1d(slicesw, chunks)), dim3(256), ldsw,
+                                       st, static_cast<const T*>(x), pk, part, events, g, tpb, slicesw, dk, gamma, gf32);
+                }
+              }
+              if (!waves)
+                hipLaunchKernelGGL((k_wgrad<T, VV, KK, CAR, SD>), dim3(blocks1d(slices, chunks)), dim3(bcg, lanes),
+                                   lds, st, static_cast<const T*>(x), pk, part, index, events, g, tpb, slices, tt, dk,
+                                   gamma, gf32);
             }
           }
           return check_launch(what);

@@ -168,7 +168,10 @@ def test_stand_alone_gradient_ops(dtype):
     assert_parity(dg[:5], rdg, torch.float32, what="grad_fused gamma")
     assert torch.count_nonzero(dg[5:]) == 0
     assert torch.equal(torch.ops.sihc.triangular_accumulate_b4_12_ptr_active5_grad_dz(g, gamma), ddz)
-    assert torch.equal(torch.ops.sihc.triangular_accumulate_b4_12_ptr_active5_grad_gamma(g, *dzs, gamma), dg)
+    # the stand-alone gamma op reduces in another (fixed) order than the fused pass
+    dg_alone = torch.ops.sihc.triangular_accumulate_b4_12_ptr_active5_grad_gamma(g, *dzs, gamma)
+    assert_parity(dg_alone[:5], rdg, torch.float32, what="grad_gamma")
+    assert torch.count_nonzero(dg_alone[5:]) == 0
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
