@@ -68,13 +68,15 @@ def parse_args():
     p.add_argument("--tri-backward", choices=("visible", "fused"), default=None,
                    help="--mode model --compile: how the triangular op's traced backward returns the update "
                         "gradients (sihc_hip.sublayer_kernels.COMPILED_TRIANGULAR_BACKWARD)")
-    p.add_argument("--mode", choices=("step", "calibrate", "kernels", "e2e", "model", "stage"), default="step",
+    p.add_argument("--mode", choices=("step", "calibrate", "kernels", "e2e", "model", "stage", "ceiling"),
+                   default="step",
                    help="step: the benchmark (default); calibrate: a 1 GiB copy-kernel launch plus single "
                         "event forward/backward launches at the same shape, for HBM counter runs; kernels: "
                         "every HIP kernel timed alone at the benchmark shape (one JSON line per kernel); e2e: "
                         "benchmark config 4, a SiHC-XL denoiser forward on a CFG batch with HIP routing; model: the "
                         "reference's fusion_profile matrix (presets x routing implementation x train/inference); "
-                        "stage: benchmark config 2 on the reference's stage API (the drop-in path) only")
+                        "stage: benchmark config 2 on the reference's stage API (the drop-in path) only; ceiling: "
+                        "the streaming ceiling rows only")
     return p.parse_args()
 
 
@@ -239,50 +241,49 @@ def _timed(torch, fn, iters=10, warmup=2):
 
 def stream_ceiling() -> dict:
     """HBM streaming ceiling of this GPU in the same run: the library's calibration stream
-    (sihc_stream: grid-stride 16-byte vectors, non-temporal loads and stores, the hints of
-    the per-event kernels) over at least 8 GiB per pass, for the read:write mixes and array
-    counts of the per-event kernels -- forward 1:1 over 4 arrays (x, dz in; x_out, z_out
-    out), backward 2:1 over 6 arrays (dX', dz', X', dz in; dX, ddz out) -- plus 1:1 over
-    2 arrays, 2:1 over 3 and write-only. Best of two grid sizes, median of 3 passes."""
+    (sihc_stream: one-shot 256-thread blocks that each move one 4 KB unit of every array,
+    16-byte vectors, non-temporal loads and stores -- the fastest pattern measured here for
+    mixed traffic). Rows: write-only, 1:1 over 2 arrays and 2:1 over 3, at 8-9 GiB per pass;
+    and the per-event kernels' own arrays at the benchmark's sizes (shapes 1 and 2:
+    carrier-shaped arrays 4 x the 151 MB workspace-shaped ones, as x / x_out / grad x are to
+    dz / z_out / grad dz; 1.5 and 2.3 GB per pass, as one launch of those kernels moves).
+    The shaped streams slow down as the arrays grow (1 GiB workspace arrays: about 8%
+    slower), so they are measured at the size the kernels see. Median of the passes after
+    one warm-up pass."""
     import torch
 
     from sihc_hip import _lib
 
     L = _lib.lib()
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    mixes = {"write-only (1 array)": (0, 1, 8 << 30), "1:1 (2 arrays)": (1, 1, 4 << 30),
-             "2:1 (3 arrays)": (2, 1, 3 << 30), "1:1 (4 arrays, the per-event forward's mix)": (2, 2, 2 << 30),
-             "2:1 (6 arrays, the per-event backward's mix)": (4, 2, 3 << 29)}
-    pool_bytes = max((nr + nw) * each for nr, nw, each in mixes.values())
-    pool = torch.empty(pool_bytes, dtype=torch.uint8, device="cuda")
-    pool.fill_(1)
-    out = {"workload": "sihc_stream over >= 8 GiB per pass (read + written), non-temporal loads and stores"}
-    for name, (nr, nw, each) in mixes.items():
-        arrays = [pool[k * each:(k + 1) * each] for k in range(nr + nw)]
-        # the kernel streams `each` bytes of every array: each slice must hold exactly that
-        if any(a.numel() != each for a in arrays):
-            raise RuntimeError(f"stream_ceiling: pool of {pool_bytes} bytes too small for {name}")
-        srcs = (ctypes.c_void_p * max(nr, 1))(*[a.data_ptr() for a in arrays[:nr]])
-        dsts = (ctypes.c_void_p * nw)(*[a.data_ptr() for a in arrays[nr:]])
-        best = None
-        for blocks in (4096, 16384):
-            fn = lambda: _lib.check(L.sihc_stream(srcs, nr, dsts, nw, each, blocks, st))  # noqa: E731
-            passes = []
-            for _ in range(4):
-                a0, b0 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                a0.record()
-                fn()
-                b0.record()
-                torch.cuda.synchronize()
-                passes.append(a0.elapsed_time(b0) * 1e-3)
-            sec = statistics.median(passes[1:])
-            gbs = (nr + nw) * each / sec / 1e9
-            if best is None or gbs > best[0]:
-                best = (gbs, blocks, sec)
-        out[name] = {"GB/s": round(best[0], 1), "frac_of_peak": round(best[0] / HBM_PEAK_GBS, 4),
-                     "bytes_per_pass": (nr + nw) * each, "ms": round(best[2] * 1e3, 3), "blocks": best[1]}
-    del pool
-    torch.cuda.empty_cache()
+    # name: (sources, destinations, shape, workspace-shaped bytes, carrier-shaped sources, destinations)
+    mixes = {"write-only (1 array)": (0, 1, 0, 8 << 30, 0, 0), "1:1 (2 arrays)": (1, 1, 0, 4 << 30, 0, 0),
+             "2:1 (3 arrays)": (2, 1, 0, 3 << 30, 0, 0),
+             "per-event forward's arrays (1:1, 10 units)": (2, 2, 1, 150994944, 1, 1),
+             "per-event backward's arrays (2:1, 15 units)": (4, 2, 2, 150994944, 2, 1)}
+    out = {"workload": "sihc_stream, one-shot 4 KB units per block, non-temporal loads and stores; generic mixes "
+                       "over 8-9 GiB per pass, the per-event kernels' arrays at the benchmark's sizes"}
+    for name, (nr, nw, shape, each, r4, w4) in mixes.items():
+        srcs_t = [torch.empty((4 if r < r4 else 1) * each, dtype=torch.uint8, device="cuda") for r in range(nr)]
+        dsts_t = [torch.empty((4 if w < w4 else 1) * each, dtype=torch.uint8, device="cuda") for w in range(nw)]
+        for t in srcs_t:
+            t.fill_(1)
+        total = sum(t.numel() for t in srcs_t + dsts_t)
+        srcs = (ctypes.c_void_p * max(nr, 1))(*[t.data_ptr() for t in srcs_t])
+        dsts = (ctypes.c_void_p * nw)(*[t.data_ptr() for t in dsts_t])
+        passes = []
+        for _ in range(4 if shape == 0 else 9):
+            a0, b0 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a0.record()
+            _lib.check(L.sihc_stream(srcs, nr, dsts, nw, each, shape, st))
+            b0.record()
+            torch.cuda.synchronize()
+            passes.append(a0.elapsed_time(b0) * 1e-3)
+        sec = statistics.median(passes[1:])
+        out[name] = {"GB/s": round(total / sec / 1e9, 1), "frac_of_peak": round(total / sec / 1e9 / HBM_PEAK_GBS, 4),
+                     "bytes_per_pass": total, "ms": round(sec * 1e3, 3)}
+        del srcs_t, dsts_t
+        torch.cuda.empty_cache()
     return out
 
 
@@ -904,6 +905,9 @@ def main():
     if args.mode == "stage":
         print(json.dumps(stage_api_config2(args.seed, max(1, args.steps), args.compile)), flush=True)
         return
+    if args.mode == "ceiling":
+        print(json.dumps(stream_ceiling()), flush=True)
+        return
     print(f"[bench] building step: batch={args.batch} C={args.channels} events={args.events}", file=sys.stderr,
           flush=True)
     step = LiteralStep(args.batch, args.channels, args.events, args.seed)
@@ -1005,9 +1009,10 @@ def main():
         result["extra"]["stream_ceiling"] = ceiling = stream_ceiling()
         fw_rate = result["fwd_kernel_GBps"]
         result["extra"]["fraction_of_stream_ceiling"] = {
-            "k_event_fwd vs 1:1 over 4 arrays": round(fw_rate / ceiling["1:1 (4 arrays, the per-event forward's mix)"]["GB/s"], 4),
-            "k_event_bwd vs 2:1 over 6 arrays": round(achieved / ceiling["2:1 (6 arrays, the per-event backward's mix)"]["GB/s"], 4),
-        }
+            "k_event_fwd vs the per-event forward's arrays":
+                round(fw_rate / ceiling["per-event forward's arrays (1:1, 10 units)"]["GB/s"], 4),
+            "k_event_bwd vs the per-event backward's arrays":
+                round(achieved / ceiling["per-event backward's arrays (2:1, 15 units)"]["GB/s"], 4)}
         torch.cuda.empty_cache()
         print("[bench] config 4 end-to-end forward", file=sys.stderr, flush=True)
         result["extra"]["config4_e2e"] = e2e_config4(args.seed)

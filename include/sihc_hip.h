@@ -39,7 +39,7 @@ extern "C" {
 #endif
 
 #define SIHC_MAX_EVENTS 32
-#define SIHC_ABI_VERSION 2
+#define SIHC_ABI_VERSION 3
 /* Bytes of the per-GPU scratch array of sihc_event_backward_noalloc (64 MiB). */
 #define SIHC_SCRATCH_BYTES (64u << 20)
 
@@ -208,14 +208,18 @@ int sihc_scatter_cells(const void *cells, const int32_t *index, void *x, int64_t
 int sihc_scatter_add_cells(const void *cells, const int32_t *index, void *x, int64_t batch,
                            int grid, int cell, int channels, int dtype, void *stream);
 
-/* Streaming calibration: reads nsrc arrays and writes ndst arrays of `bytes` bytes each
- * (16-byte aligned, bytes a multiple of 16) with a grid-stride loop of `blocks` 256-thread
- * blocks and non-temporal loads and stores; dst_j = XOR of the sources ^ j (write-only:
- * an index pattern). Mixes 0:1, 1:1, 2:1, 2:2 and 4:2 (the per-event kernels move their
- * bytes 1:1 and 2:1 over 4 and 6 arrays). No reference counterpart: the HBM ceiling the per-event kernels are read
- * against. */
+/* Streaming calibration in the fastest measured pattern for mixed traffic (one-shot
+ * 256-thread blocks that each move one 4 KB unit of every array, 16-byte vectors,
+ * non-temporal loads and stores); dst_j = XOR of the sources (write-only: an index
+ * pattern). `bytes` (a multiple of 4096) is the size of a workspace-shaped array.
+ * shape 0: nsrc:ndst equal arrays of `bytes` (0:1, 1:1, 2:1, 2:2, 4:2);
+ * shape 1: the per-event forward's arrays -- sources {carrier, workspace}, destinations
+ *          {carrier, workspace}, carriers 4 x `bytes` (1:1, 10 units);
+ * shape 2: the per-event backward's arrays -- sources {carrier, carrier, workspace,
+ *          workspace}, destinations {carrier, workspace} (2:1, 15 units).
+ * No reference counterpart: the HBM ceiling the per-event kernels are read against. */
 int sihc_stream(const void *const *src, int nsrc, void *const *dst, int ndst, size_t bytes,
-                int blocks, void *stream);
+                int shape, void *stream);
 
 /* Plain device copy of `bytes` bytes (16-byte vectors). No reference counterpart: it is
  * the calibration kernel for HBM counters and the practical bandwidth ceiling. */

@@ -144,12 +144,18 @@ def test_deferred_finalize_arguments_are_validated():
 def test_stream_calibration_arguments_are_validated():
     lib = _lib.lib()
     arr = _lib.ptr_array([FAKE, FAKE])
-    assert lib.sihc_stream(arr, 3, arr, 1, 1 << 20, 1024, None) == 1
+    assert lib.sihc_stream(arr, 3, arr, 1, 1 << 20, 0, None) == 1
     assert b"unsupported mix" in lib.sihc_last_error()
-    assert lib.sihc_stream(arr, 1, arr, 1, 1000, 1024, None) == 1
-    assert b"multiple of 16" in lib.sihc_last_error()
-    assert lib.sihc_stream(_lib.ptr_array([FAKE + 8]), 1, arr, 1, 1 << 20, 1024, None) == 1
+    assert lib.sihc_stream(arr, 1, arr, 1, 1000, 0, None) == 1
+    assert b"multiple of 4096" in lib.sihc_last_error()
+    assert lib.sihc_stream(_lib.ptr_array([FAKE + 8]), 1, arr, 1, 1 << 20, 0, None) == 1
     assert b"misaligned" in lib.sihc_last_error()
+    assert lib.sihc_stream(arr, 1, arr, 1, 1 << 20, 3, None) == 1
+    assert b"shape must be" in lib.sihc_last_error()
+    assert lib.sihc_stream(arr, 2, arr, 1, 1 << 20, 1, None) == 1
+    assert b"shape 1 takes" in lib.sihc_last_error()
+    assert lib.sihc_stream(arr, 2, arr, 2, 1 << 20, 2, None) == 1
+    assert b"shape 2 takes" in lib.sihc_last_error()
 
 
 def test_oversized_tensor_is_rejected():

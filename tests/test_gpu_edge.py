@@ -114,31 +114,47 @@ def test_sixteen_slot_cells_at_batch_32():
     assert_parity(wg[:, :32], exp.to(bf), bf, what="p4 weight grad (channel slice)", kind="reduced")
 
 
-@pytest.mark.parametrize("nr,nw", [(0, 1), (1, 1), (2, 1), (2, 2), (4, 2)])
-def test_stream_calibration_kernel(nr, nw):
-    # sihc_stream (the HBM ceiling the bench reports): dst_j = XOR of the sources ^ j, and
-    # the write-only mix stores the 16-byte vector index pattern
+STREAM_CASES = [(0, 1, 0), (1, 1, 0), (2, 1, 0), (2, 2, 0), (4, 2, 0), (2, 2, 1), (4, 2, 2)]
+
+
+@pytest.mark.parametrize("nr,nw,shape", STREAM_CASES, ids=[f"{r}:{w}-shape{s}" for r, w, s in STREAM_CASES])
+def test_stream_calibration_kernel(nr, nw, shape):
+    # sihc_stream (the HBM ceiling the bench reports). Unit u (4 KB of a workspace-shaped
+    # array, 16 KB of a carrier-shaped one), thread t: acc = {u, t, 0, 0} XOR every vector
+    # the thread loads (vector u*256 + t of a workspace-shaped source, u*1024 + q*256 + t,
+    # q < 4, of a carrier-shaped one); destination j gets acc ^ j, or acc ^ (4j + q) for
+    # carrier-shaped ones. Shapes 1 and 2: the first source(s) and the first destination
+    # are carrier-shaped (1 and 2 carrier sources).
     import ctypes
 
     from sihc_hip import _lib
 
-    announce(f"stream calibration {nr}:{nw}")
+    announce(f"stream calibration {nr}:{nw} shape {shape}")
     L = _lib.lib()
-    n = (1 << 20) + 16 * 7  # bytes: not a multiple of the grid's stride
-    g = torch.Generator(device="cuda").manual_seed(nr * 10 + nw)
-    srcs = [torch.randint(0, 2 ** 31 - 1, (n // 4,), device="cuda", generator=g, dtype=torch.int32) for _ in range(nr)]
-    dsts = [torch.zeros(n // 4, device="cuda", dtype=torch.int32) for _ in range(nw)]
+    units = 37
+    n = 4096 * units
+    r4 = {0: 0, 1: 1, 2: 2}[shape]
+    w4 = 0 if shape == 0 else 1
+    g = torch.Generator(device="cuda").manual_seed(nr * 10 + nw + 100 * shape)
+    rint = lambda m: torch.randint(0, 2 ** 31 - 1, (m * n // 4,), device="cuda", generator=g, dtype=torch.int32)  # noqa
+    srcs = [rint(4 if r < r4 else 1) for r in range(nr)]
+    dsts = [torch.zeros((4 if w < w4 else 1) * n // 4, device="cuda", dtype=torch.int32) for w in range(nw)]
     sp = (ctypes.c_void_p * max(nr, 1))(*[t.data_ptr() for t in srcs])
     dp = (ctypes.c_void_p * nw)(*[t.data_ptr() for t in dsts])
-    _lib.check(L.sihc_stream(sp, nr, dp, nw, n, 64, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    _lib.check(L.sihc_stream(sp, nr, dp, nw, n, shape, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
     torch.cuda.synchronize()
-    if nr:
-        acc = srcs[0].clone()
-        for t in srcs[1:]:
-            acc ^= t
-    else:
-        idx = torch.arange(n // 16, device="cuda", dtype=torch.int64)
-        acc = torch.stack([idx & 0xFFFFFFFF, idx >> 32, torch.zeros_like(idx), torch.zeros_like(idx)], 1)
-        acc = acc.to(torch.int64).view(-1).to(torch.int32)
+    acc = torch.zeros(units, 256, 4, device="cuda", dtype=torch.int32)
+    acc[:, :, 0] = torch.arange(units, device="cuda", dtype=torch.int32)[:, None]
+    acc[:, :, 1] = torch.arange(256, device="cuda", dtype=torch.int32)[None, :]
+    for r, t in enumerate(srcs):
+        if r < r4:
+            for q in range(4):
+                acc ^= t.view(units, 4, 256, 4)[:, q]
+        else:
+            acc ^= t.view(units, 256, 4)
     for j, d in enumerate(dsts):
-        assert torch.equal(d, acc ^ j), f"output {j}"
+        if j < w4:
+            for q in range(4):
+                assert torch.equal(d.view(units, 4, 256, 4)[:, q], acc ^ (4 * j + q)), f"output {j} slot {q}"
+        else:
+            assert torch.equal(d.view(units, 256, 4), acc ^ j), f"output {j}"
