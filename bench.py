@@ -641,9 +641,22 @@ def kernels(args) -> None:
     h = r((B, edge, edge, C), 0.0, 1e-2)
     cases.append(("event_backward", (3 * S + 3) * U,
                   lambda: launch.event_backward(h, ws[1], x, ws[0], beta[0], alpha[1])))
-    cp_src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    cp_dst = torch.empty_like(cp_src)
-    cases.append(("copy 1 GiB (read+write ceiling)", 2 << 30, lambda: launch.copy_(cp_dst, cp_src)))
+    # reference rows: the calibration stream over the per-event kernels' own arrays (one
+    # 4-slot carrier-shaped array is 4 workspace-shaped ones; U bytes each)
+    from sihc_hip import _lib
+
+    Lk = _lib.lib()
+    stv = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    carriers = [torch.empty(4 * U, dtype=torch.uint8, device=dev) for _ in range(3)]
+    wss = [torch.empty(U, dtype=torch.uint8, device=dev) for _ in range(4)]
+    arr = lambda ts: (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])  # noqa: E731
+    f_src, f_dst = arr([carriers[0], wss[0]]), arr([carriers[1], wss[1]])
+    b_src, b_dst = arr([carriers[0], carriers[1], wss[0], wss[1]]), arr([carriers[2], wss[2]])
+    if S == 4:
+        cases.append(("stream, the per-event forward's arrays (reference)", 10 * U,
+                      lambda: _lib.check(Lk.sihc_stream(f_src, 2, f_dst, 2, U, 1, stv))))
+        cases.append(("stream, the per-event backward's arrays (reference)", 15 * U,
+                      lambda: _lib.check(Lk.sihc_stream(b_src, 4, b_dst, 2, U, 2, stv))))
     xb = x[: B // 2].contiguous()
     idx = group_index(B // 2, 16, 5, seed=3).to(dev)
     cells = launch.gather_cells(xb, idx, S)
