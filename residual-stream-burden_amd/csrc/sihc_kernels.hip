@@ -1900,7 +1900,13 @@ int wgrad_chunks(int64_t M, int events, int C) {
   const int64_t cap = std::max<int64_t>(1, std::min<int64_t>(M / 32, 2048));
   return int(std::max<int64_t>(base, std::min(want, cap)));
 }
-int event_bwd_chunks(int64_t M) { return chunk_count(M, SIHC_EV_CHUNK, SIHC_EV_MAXCHUNKS); }
+// Reduction chunks of the per-event backward: 4-slot cells one per SIHC_EV_CHUNK tokens up
+// to SIHC_EV_MAXCHUNKS; 16-slot cells, whose partial rows are 4x larger per chunk, one per
+// 2 x SIHC_EV_CHUNK tokens up to half as many.
+int event_bwd_chunks(int64_t M, int cell) {
+  return cell == 2 ? chunk_count(M, SIHC_EV_CHUNK, SIHC_EV_MAXCHUNKS)
+                   : chunk_count(M, 2 * SIHC_EV_CHUNK, SIHC_EV_MAXCHUNKS / 2);
+}
 // Token chunks of the fused triangular backward (which also stores the update
 // gradients): one per SIHC_TRIB_CHUNK tokens up to 1024, at least the weight-gradient
 // count. Shorter runs per block stream through a narrower window of each array (A = 3:
@@ -2719,7 +2725,7 @@ int sihc_event_forward(const void* x, const void* dz, const void* beta, const vo
 size_t sihc_event_backward_workspace_size(int64_t batch, int grid, int cell, int channels) {
   if (batch < 0 || grid <= 0 || cell <= 0 || channels <= 0) return 0;
   const int64_t M = batch * int64_t(grid) * grid;
-  return size_t(event_bwd_chunks(M)) * 2 * cell * cell * channels * sizeof(float);
+  return size_t(event_bwd_chunks(M, cell)) * 2 * cell * cell * channels * sizeof(float);
 }
 
 // sihc_event_backward and its allocation-free variant (errors name the entry point)
@@ -2755,7 +2761,7 @@ static int event_backward_impl(const char* what, const void* grad_x_out, const v
   if (!has_w && !has_g) return fail(SIHC_ERR_INVALID, "%s: neither a write nor a read part", what);
   if (!grad_x && has_g)
     return fail(SIHC_ERR_INVALID, "%s: grad_x may be NULL only without grad_z_out (it equals grad_x_out)", what);
-  const int max_chunks = event_bwd_chunks(g.M);
+  const int max_chunks = event_bwd_chunks(g.M, cell);
   const size_t need = size_t(max_chunks) * 2 * S * channels * sizeof(float);
   if (!workspace || workspace_bytes < need)
     return fail(SIHC_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", what, need, workspace_bytes);
@@ -2902,7 +2908,7 @@ int sihc_event_backward_noalloc(const void* grad_x_out, const void* grad_z_out, 
   Geo g;
   if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
   // the partial rows the launch may use (its chunk count never exceeds this one)
-  const size_t need = size_t(event_bwd_chunks(g.M)) * 2 * cell * cell * size_t(channels) * sizeof(float);
+  const size_t need = size_t(event_bwd_chunks(g.M, cell)) * 2 * cell * cell * size_t(channels) * sizeof(float);
   if (need > size_t(SIHC_SCRATCH_BYTES))
     return fail(SIHC_ERR_INVALID,
                 "%s: these sizes need %zu bytes of reduction scratch, more than the %zu-byte array this entry point "
