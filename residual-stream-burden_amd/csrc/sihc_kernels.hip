@@ -1323,55 +1323,75 @@ __global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgradz(const bf16_t* __
 // goes to out0 + r*C*S ([R][C][S], `pair` == 0) or, with `pair`, row 0 -> out0 and
 // row 1 -> out1 (each [C][S]). Rows whose bit is set in zero_mask are written as
 // zeros without reading partials; a NULL destination row is skipped.
-// Block: 32 outputs x 8 chunk groups; each group sums its chunks in ascending order,
-// then the 8 group sums are added in ascending group order.
+// Block: 32 x NV outputs x 8 chunk groups; each group sums its chunks in ascending
+// order, then the 8 group sums are added in ascending group order. With NV = 4 a thread
+// reads four neighbouring outputs of each partial row as one 16-byte load (the group's
+// lanes then read 512 contiguous bytes per row instead of 128); the sums, and so the
+// bits, do not depend on NV.
 // ----------------------------------------------------------------------------------
-template <typename TO>
+template <typename TO, int NV>
 __device__ __forceinline__ void finalize_outputs(const float* __restrict__ part, TO* __restrict__ out0,
                                                  TO* __restrict__ out1, int chunks, int R, int S, int C, int pair,
                                                  int zero_mask, int block) {
   constexpr int FO = 32, FG = 8;
-  __shared__ float red[FG][FO];
-  const int64_t n = int64_t(R) * S * C;
+  __shared__ float red[FG][FO * NV];
+  const int64_t n = int64_t(R) * S * C, SC = int64_t(S) * C;  // NV > 1: SC % NV == 0
   const int o = threadIdx.x % FO, grp = threadIdx.x / FO;
-  const int64_t i = int64_t(block) * FO + o;
-  const int r = i < n ? int(i / (int64_t(S) * C)) : 0;
+  const int64_t i = (int64_t(block) * FO + o) * NV;  // this thread's first output
+  const bool live = i < n;
+  const int r = live ? int(i / SC) : 0;  // the NV outputs share the row r
   const bool zero = (zero_mask >> r) & 1;
-  float sum = 0.f;
-  if (i < n && !zero) {
+  float sum[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) sum[j] = 0.f;
+  if (live && !zero) {
     // 8 independent loads in flight per thread; the sum order stays ascending in k.
     int k = grp;
     for (; k + 7 * FG < chunks; k += 8 * FG) {
-      float v[8];
+      float v[8][NV];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] = part[int64_t(k + q * FG) * n + i];
+      for (int q = 0; q < 8; ++q) load_vec<float, NV>(part + int64_t(k + q * FG) * n + i, v[q]);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) sum += v[q];
+      for (int q = 0; q < 8; ++q)
+#pragma unroll
+        for (int j = 0; j < NV; ++j) sum[j] += v[q][j];
     }
-    for (; k < chunks; k += FG) sum += part[int64_t(k) * n + i];
-  }
-  red[grp][o] = sum;
-  __syncthreads();
-  if (grp != 0 || i >= n) return;
-  float t = 0.f;
+    for (; k < chunks; k += FG) {
+      float v[NV];
+      load_vec<float, NV>(part + int64_t(k) * n + i, v);
 #pragma unroll
-  for (int q = 0; q < FG; ++q) t += red[q][o];
-  const int rem = int(i - int64_t(r) * S * C);
-  const int s = rem / C;
-  const int c = rem - s * C;
+      for (int j = 0; j < NV; ++j) sum[j] += v[j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j) red[grp][o * NV + j] = sum[j];
+  __syncthreads();
+  if (grp != 0 || !live) return;
   TO* dst = pair ? (r == 0 ? out0 : out1) : (out0 ? out0 + int64_t(r) * C * S : nullptr);
-  if (dst) dst[int64_t(c) * S + s] = from_f32<TO>(zero ? 0.f : t);
+  if (!dst) return;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    float t = 0.f;
+#pragma unroll
+    for (int q = 0; q < FG; ++q) t += red[q][o * NV + j];
+    const int rem = int(i + j - int64_t(r) * SC);
+    const int s = rem / C;
+    const int c = rem - s * C;
+    dst[int64_t(c) * S + s] = from_f32<TO>(zero ? 0.f : t);
+  }
 }
 
-template <typename TO>
+template <typename TO, int NV>
 __global__ void __launch_bounds__(256) k_finalize(const float* __restrict__ part, TO* __restrict__ out0,
                                                   TO* __restrict__ out1, int chunks, int R, int S, int C,
                                                   int pair, int zero_mask) {
-  finalize_outputs<TO>(part, out0, out1, chunks, R, S, C, pair, zero_mask, int(blockIdx.x));
+  finalize_outputs<TO, NV>(part, out0, out1, chunks, R, S, C, pair, zero_mask, int(blockIdx.x));
 }
 
 // The per-event backward's finalize for up to SIHC_FINALIZE_BATCH deferred events in one
 // launch (grid.y = event): the same fixed-order sums as k_finalize, so the same bits.
+// Partial rows of the per-event backward are 16-byte aligned with 2 x S x C (S = 4 or 16)
+// entries, so every event takes the 4-wide path.
 #define SIHC_FINALIZE_BATCH 32
 struct FinalizeBatch {
   const float* part[SIHC_FINALIZE_BATCH];
@@ -1384,8 +1404,8 @@ struct FinalizeBatch {
 template <typename TO>
 __global__ void __launch_bounds__(256) k_finalize_batch(FinalizeBatch b, int S, int C) {
   const int e = int(blockIdx.y);
-  finalize_outputs<TO>(b.part[e], static_cast<TO*>(b.out0[e]), static_cast<TO*>(b.out1[e]), b.chunks[e], 2, S, C,
-                       1, b.zero_mask[e], int(blockIdx.x));
+  finalize_outputs<TO, 4>(b.part[e], static_cast<TO*>(b.out0[e]), static_cast<TO*>(b.out1[e]), b.chunks[e], 2, S, C,
+                          1, b.zero_mask[e], int(blockIdx.x));
 }
 
 template <typename TO>
@@ -2102,13 +2122,24 @@ int fill_zero(int dtype, void* out, int64_t n, hipStream_t st, const char* what)
 int launch_finalize(const char* what, const float* part, void* out0, void* out1, int chunks, int R, int S, int C,
                     bool pair, int zero_mask, int out_dtype, hipStream_t st) {
   const int64_t n = int64_t(R) * S * C;
-  const unsigned blocks = unsigned((n + 31) / 32);
-  if (out_dtype == SIHC_DTYPE_F32) {
-    hipLaunchKernelGGL((k_finalize<float>), dim3(blocks), dim3(256), 0, st, part, static_cast<float*>(out0),
-                       static_cast<float*>(out1), chunks, R, S, C, pair ? 1 : 0, zero_mask);
+  // 4 outputs per thread when they never straddle a row and the rows are 16-byte aligned
+  const bool wide = (int64_t(S) * C) % 4 == 0 && aligned(part, 16);
+  auto go = [&](auto nv) {
+    constexpr int NV = decltype(nv)::value;
+    const unsigned blocks = unsigned((n + 32 * NV - 1) / (32 * NV));
+    if (out_dtype == SIHC_DTYPE_F32) {
+      hipLaunchKernelGGL((k_finalize<float, NV>), dim3(blocks), dim3(256), 0, st, part, static_cast<float*>(out0),
+                         static_cast<float*>(out1), chunks, R, S, C, pair ? 1 : 0, zero_mask);
+    } else {
+      hipLaunchKernelGGL((k_finalize<bf16_t, NV>), dim3(blocks), dim3(256), 0, st, part,
+                         static_cast<bf16_t*>(out0), static_cast<bf16_t*>(out1), chunks, R, S, C, pair ? 1 : 0,
+                         zero_mask);
+    }
+  };
+  if (wide) {
+    go(std::integral_constant<int, 4>{});
   } else {
-    hipLaunchKernelGGL((k_finalize<bf16_t>), dim3(blocks), dim3(256), 0, st, part, static_cast<bf16_t*>(out0),
-                       static_cast<bf16_t*>(out1), chunks, R, S, C, pair ? 1 : 0, zero_mask);
+    go(std::integral_constant<int, 1>{});
   }
   return check_launch(what);
 }
@@ -2875,7 +2906,7 @@ int sihc_event_finalize(int n, const void* const* workspaces, const int* info, v
       return fail(SIHC_ERR_INVALID, "%s: null gradient of event %d", what, i);
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const unsigned bx = unsigned((int64_t(2) * S * channels + 31) / 32);
+  const unsigned bx = unsigned((int64_t(2) * S * channels + 127) / 128);  // 128 outputs per block
   for (int i0 = 0; i0 < n; i0 += SIHC_FINALIZE_BATCH) {
     FinalizeBatch b{};
     int nb = 0;
