@@ -122,6 +122,15 @@
 #ifndef SIHC_K4_BF16W  // 1: 16-slot read / write stage bf16 weights packed as bf16 in LDS
 #define SIHC_K4_BF16W 1
 #endif
+#ifndef SIHC_K4_DOT2  // 1: 16-slot bf16 read / write / weight gradient sum bf16 pairs with v_dot2c_f32_bf16
+#define SIHC_K4_DOT2 1
+#endif
+#ifndef SIHC_RD2_U  // tokens per lane per iteration of the 16-slot dot2 read
+#define SIHC_RD2_U 4
+#endif
+#ifndef SIHC_WR2_U  // tokens per lane per iteration of the 16-slot dot2 write
+#define SIHC_WR2_U 2
+#endif
 #ifndef SIHC_K2_BF16W  // the same for 4-slot read / write (8-channel lanes)
 #define SIHC_K2_BF16W 1
 #endif
@@ -565,6 +574,128 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict_
 }
 
 // ----------------------------------------------------------------------------------
+// bf16 pair arithmetic (16-slot cells). A 32-bit word holds two bf16 values; pair_lo /
+// pair_hi gather the low / high halves of two words into one word (v_perm_b32), and
+// dot2 adds both products of two such words to an fp32 accumulator (v_dot2c_f32_bf16:
+// the bf16 products are exact in fp32), so one VALU instruction does two multiply-adds.
+// ----------------------------------------------------------------------------------
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pair_lo(uint32_t a, uint32_t b) {  // a.lo | b.lo << 16
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pair_hi(uint32_t a, uint32_t b) {  // a.hi | b.hi << 16
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), acc,
+                                         false);
+}
+
+// Stage the read weights of a 2-channel-lane slice [cs, cs + 2*BCG) for the dot2 read:
+// alpha [E][C][16] bf16 holds, for each (e, c), the 8 slot-pair words (slots 2p, 2p+1)
+// the read multiplies against. LDS layout [e][q][lane][4]: words (pair 2q, channel 0),
+// (2q, 1), (2q + 1, 0), (2q + 1, 1), so a lane reads an event's 16 words with four
+// consecutive-address 16-byte reads. Channels past C get zero words.
+__device__ __forceinline__ void stage_read_pairs(uint32_t* lds, const bf16_t* __restrict__ alpha, int E, int BCG,
+                                                 int cs, int C) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(alpha);
+  const int BC = 2 * BCG;
+  const int tid = threadIdx.y * blockDim.x + threadIdx.x;
+  const int nthr = blockDim.x * blockDim.y;
+  for (int i = tid; i < E * BC * 8; i += nthr) {  // global [e][c][pair]: coalesced
+    const int e = i / (BC * 8);
+    const int r = i - e * BC * 8;
+    const int cl = r >> 3, pr = r & 7;
+    const int c = cs + cl;
+    lds[((e * 4 + (pr >> 1)) * BCG + (cl >> 1)) * 4 + (pr & 1) * 2 + (cl & 1)] =
+        c < C ? w[(int64_t(e) * C + c) * 8 + pr] : 0u;
+  }
+  __syncthreads();
+}
+
+// ----------------------------------------------------------------------------------
+// 16-slot read in bf16: out_e[m,c] = sum_s alpha[e,c,s] * x[m,s,c] with the slot sum done
+// in pairs by dot2. A lane owns 2 channels (one word per token and slot) and U tokens;
+// each token's 16 slot words become 8 pair words per channel (pair_lo / pair_hi), which
+// then serve all E events. Per event and token a lane issues 16 dot2 (the fp32 kernel:
+// 32 FMAs plus the bf16 -> fp32 unpacking of its weights), and each 16-byte LDS weight
+// read feeds U tokens. Same block shape, token runs and hints as k_read.
+// ----------------------------------------------------------------------------------
+template <int U, int BCGT, int NTM>
+__global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read_d2(const bf16_t* __restrict__ x,
+                                                 const bf16_t* __restrict__ alpha, PtrPack out,
+                                                 const int32_t* __restrict__ index, int E, Geo g, int gs,
+                                                 int nchunks, int nslices) {
+  constexpr int K = 4, S = 16;
+  constexpr bool NTL = (NTM & 1) != 0, NTS = (NTM & 2) != 0;  // hints: loads, stores
+  extern __shared__ float lds[];
+  const int BCG = BCGT ? BCGT : int(blockDim.x), TL = blockDim.y;
+  const int blk = logical_block<true>(), slice = blk % nslices, chunk = blk / nslices;
+  const int cs = slice * BCG * 2;
+  stage_read_pairs(reinterpret_cast<uint32_t*>(lds), alpha, E, BCG, cs, g.C);
+  const u32x4* wl = reinterpret_cast<const u32x4*>(lds);
+  const int c0 = cs + threadIdx.x * 2;
+  if (c0 >= g.C) return;
+  // slot s of a cell: carrier row s / 4, pixel s % 4 of the cell's 4-pixel run; in words
+  // (2 channels each, C even on this path) a pixel is C / 2 words and a row GK * C / 2
+  const int64_t row_w = int64_t(g.GK) * (g.C >> 1);
+  const int pix_w = g.C >> 1;
+  for (int64_t m0 = int64_t(chunk) * gs; m0 < g.M; m0 += int64_t(nchunks) * gs) {
+    const int64_t m_end = min(m0 + gs, int64_t(g.M));
+    for (int64_t mi = m0; mi < m_end; mi += U * TL) {
+      const int64_t m = mi + threadIdx.y;
+      bool ok[U];
+      int64_t zoff[U];
+      uint32_t xw[U][S];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        ok[u] = m + u * TL < m_end;
+        const int mu = int(ok[u] ? m + u * TL : mi);  // tail: reload a valid token, store nothing
+        const uint32_t* px = reinterpret_cast<const uint32_t*>(x + cell_pixel0(mu, g, index) * g.C + c0);
+        zoff[u] = int64_t(mu) * g.C + c0;
+#pragma unroll
+        for (int uy = 0; uy < K; ++uy)
+#pragma unroll
+          for (int ux = 0; ux < K; ++ux) xw[u][uy * K + ux] = ld<NTL>(px + uy * row_w + ux * pix_w);
+      }
+      load_fence();
+      uint32_t xp[U][S / 2][2];  // [token][slot pair][channel]
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int pr = 0; pr < S / 2; ++pr) {
+          xp[u][pr][0] = pair_lo(xw[u][2 * pr], xw[u][2 * pr + 1]);
+          xp[u][pr][1] = pair_hi(xw[u][2 * pr], xw[u][2 * pr + 1]);
+        }
+      for (int e = 0; e < E; ++e) {
+        float acc[U][2];
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc[u][0] = acc[u][1] = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const u32x4 w = wl[(e * 4 + q) * BCG + threadIdx.x];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            acc[u][0] = dot2(xp[u][2 * q][0], w[0], acc[u][0]);
+            acc[u][1] = dot2(xp[u][2 * q][1], w[1], acc[u][1]);
+            acc[u][0] = dot2(xp[u][2 * q + 1][0], w[2], acc[u][0]);
+            acc[u][1] = dot2(xp[u][2 * q + 1][1], w[3], acc[u][1]);
+          }
+        }
+        // all U chains are computed before the tail test (otherwise the compiler moves each
+        // token's chain into its store's branch, leaving two dependent chains at a time)
+#pragma unroll
+        for (int u = 0; u < U; ++u) asm volatile("" : "+v"(acc[u][0]), "+v"(acc[u][1]));
+        bf16_t* dst = static_cast<bf16_t*>(const_cast<void*>(out.p[e]));
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (ok[u]) store_vec<bf16_t, 2, NTS>(dst + zoff[u], acc[u]);
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------
 // write: out[m,s,c] = (add_x ? x : 0) + sum_e beta[e,c,s] * upd_e[m,c]
 // Events are consumed in groups of 4 (E padded to a multiple of 4 with zero weights
 // and a repeated valid pointer), so each group's 4 update loads issue together.
@@ -673,6 +804,138 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restric
         for (int s = 0; s < S; ++s) store_vec<TX, V, NTS>(out + slot_offset<K>(p0[u], s, g, c0), acc[u][s]);
       }
   }
+  }
+}
+
+// Stage the write weights of a 2-channel-lane slice for the dot2 write: word (j, s, c) =
+// beta[2j][c][s] | beta[2j + 1][c][s] << 16, the event pair j's weights of slot s (a zero
+// high half past the last event). LDS layout [j][s / 2][lane][4]: words (s even, channel
+// 0), (s even, 1), (s odd, 0), (s odd, 1), so a lane reads a pair's 32 words with eight
+// consecutive-address 16-byte reads.
+__device__ __forceinline__ void stage_write_pairs(uint32_t* lds, const bf16_t* __restrict__ beta, int E, int BCG,
+                                                  int cs, int C) {
+  const uint16_t* w = reinterpret_cast<const uint16_t*>(beta);
+  const int BC = 2 * BCG, J = (E + 1) / 2;
+  const int tid = threadIdx.y * blockDim.x + threadIdx.x;
+  const int nthr = blockDim.x * blockDim.y;
+  for (int i = tid; i < J * BC * 16; i += nthr) {  // [j][c][s]: consecutive slots of one (e, c)
+    const int j = i / (BC * 16);
+    const int r = i - j * BC * 16;
+    const int cl = r >> 4, sl = r & 15;
+    const int c = cs + cl;
+    uint32_t lo = 0u, hi = 0u;
+    if (c < C) {
+      lo = w[(int64_t(2 * j) * C + c) * 16 + sl];
+      if (2 * j + 1 < E) hi = w[(int64_t(2 * j + 1) * C + c) * 16 + sl];
+    }
+    lds[((j * 8 + (sl >> 1)) * BCG + (cl >> 1)) * 4 + (sl & 1) * 2 + (cl & 1)] = lo | (hi << 16);
+  }
+  __syncthreads();
+}
+
+// ----------------------------------------------------------------------------------
+// 16-slot write in bf16: out[m,s,c] = (add_x ? x[m,s,c] : 0) + sum_e beta[e,c,s] *
+// upd_e[m,c], the event sum done in pairs by dot2. A lane owns 2 channels and U tokens
+// (16 x 2 fp32 accumulators per token, started from the carrier when add_x); each event
+// pair's two update words per token become one pair word per channel (pair_lo /
+// pair_hi), multiplied against the staged weight pair of every slot: 32 dot2 per token
+// and pair (the fp32 kernel: 64 FMAs plus weight unpacking). The next pair's update
+// words are loaded before the current pair is summed. Same block shape, token runs and
+// hints as k_write.
+// ----------------------------------------------------------------------------------
+template <int U, bool ADD_X, int BCGT, int NTM>
+__global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write_d2(const bf16_t* __restrict__ x, PtrPack upd,
+                                                  const bf16_t* __restrict__ beta, bf16_t* __restrict__ out,
+                                                  const int32_t* __restrict__ index, int E, Geo g, int gs,
+                                                  int nchunks, int nslices) {
+  constexpr int K = 4, S = 16;
+  constexpr bool NTL = (NTM & 1) != 0, NTS = (NTM & 2) != 0;  // hints: loads, stores
+  extern __shared__ float lds[];
+  const int BCG = BCGT ? BCGT : int(blockDim.x), TL = blockDim.y;
+  const int blk = logical_block<true>(), slice = blk % nslices, chunk = blk / nslices;
+  const int cs = slice * BCG * 2;
+  stage_write_pairs(reinterpret_cast<uint32_t*>(lds), beta, E, BCG, cs, g.C);
+  const u32x4* wl = reinterpret_cast<const u32x4*>(lds);
+  const int c0 = cs + threadIdx.x * 2;
+  if (c0 >= g.C) return;
+  const int J = (E + 1) / 2;
+  // carrier words (2 channels each, C even on this path): a pixel is C / 2 words, a
+  // carrier row GK * C / 2
+  const int64_t row_w = int64_t(g.GK) * (g.C >> 1);
+  const int pix_w = g.C >> 1;
+  const uint32_t* xw = reinterpret_cast<const uint32_t*>(x);
+  uint32_t* ow = reinterpret_cast<uint32_t*>(out);
+  for (int64_t m0 = int64_t(chunk) * gs; m0 < g.M; m0 += int64_t(nchunks) * gs) {
+    const int64_t m_end = min(m0 + gs, int64_t(g.M));
+    for (int64_t mi = m0; mi < m_end; mi += U * TL) {
+      const int64_t m = mi + threadIdx.y;
+      bool ok[U];
+      int64_t zoff[U], b0[U];
+      float acc[U][S][2];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        ok[u] = m + u * TL < m_end;
+        const int mu = int(ok[u] ? m + u * TL : mi);  // tail: reload a valid token, store nothing
+        b0[u] = (cell_pixel0(mu, g, index) * g.C + c0) >> 1;
+        zoff[u] = int64_t(mu) * g.C + c0;
+        if constexpr (ADD_X) {
+#pragma unroll
+          for (int uy = 0; uy < K; ++uy)
+#pragma unroll
+            for (int ux = 0; ux < K; ++ux) {
+              const uint32_t v = ld<NTL>(xw + b0[u] + uy * row_w + ux * pix_w);
+              acc[u][uy * K + ux][0] = __uint_as_float(v << 16);
+              acc[u][uy * K + ux][1] = __uint_as_float(v & 0xffff0000u);
+            }
+        } else {
+#pragma unroll
+          for (int s = 0; s < S; ++s) acc[u][s][0] = acc[u][s][1] = 0.f;
+        }
+      }
+      uint32_t zr[2][U];  // update words of the next event pair: [event of the pair][token]
+      auto issue = [&](int j) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const bf16_t* z = static_cast<const bf16_t*>(upd.p[min(2 * j + q, E - 1)]);
+#pragma unroll
+          for (int u = 0; u < U; ++u) zr[q][u] = ld<NTL>(reinterpret_cast<const uint32_t*>(z + zoff[u]));
+        }
+      };
+      issue(0);
+      for (int j = 0; j < J; ++j) {
+        uint32_t d[U][2];  // [token][channel]: (event 2j, event 2j + 1) pair words
+        const bool second = 2 * j + 1 < E;  // past the last event the pair's high half is zero
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const uint32_t w1 = second ? zr[1][u] : 0u;
+          d[u][0] = pair_lo(zr[0][u], w1);
+          d[u][1] = pair_hi(zr[0][u], w1);
+        }
+        if (j + 1 < J) issue(j + 1);
+        load_fence();
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const u32x4 w = wl[(j * 8 + q) * BCG + threadIdx.x];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            acc[u][2 * q][0] = dot2(d[u][0], w[0], acc[u][2 * q][0]);
+            acc[u][2 * q][1] = dot2(d[u][1], w[1], acc[u][2 * q][1]);
+            acc[u][2 * q + 1][0] = dot2(d[u][0], w[2], acc[u][2 * q + 1][0]);
+            acc[u][2 * q + 1][1] = dot2(d[u][1], w[3], acc[u][2 * q + 1][1]);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (ok[u]) {
+#pragma unroll
+          for (int uy = 0; uy < K; ++uy)
+#pragma unroll
+            for (int ux = 0; ux < K; ++ux)
+              store_vec<bf16_t, 2, NTS>(reinterpret_cast<bf16_t*>(ow + b0[u] + uy * row_w + ux * pix_w),
+                                        acc[u][uy * K + ux]);
+        }
+    }
   }
 }
 
@@ -2452,6 +2715,9 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
   const bool wb = dtype == SIHC_DTYPE_BF16 &&
                   ((SIHC_K4_BF16W && cell == 4 && V == 2) || (SIHC_K2_BF16W && cell == 2 && V == 8));
   const int wbytes = wb ? 2 : 4;
+  // 16 slots, bf16, 2-channel lanes, word-aligned weights: slot pairs summed by dot2 (the
+  // weights' pair words staged in the same LDS bytes as the packed bf16 weights)
+  const bool d2 = SIHC_K4_DOT2 && wb && cell == 4 && aligned(alpha, 4);
   const Shape2D sh = cell == 2 ? shape_for(channels, V, SIHC_RW_BCG, events * S * wbytes)
                                : shape_for(channels, V, SIHC_RW_BCG_K4, events * S * wbytes, SIHC_RW_LDS_K4);
   const int tpb = sh.tl * rw_tokens_per_lane(cell, events, true);
@@ -2485,6 +2751,15 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
                                      static_cast<const T*>(alpha), pk, index, events, g, gs, int(chunks), sh.slices);
                   return check_launch(what);
                 };
+                if constexpr (KK == 4 && VV == 2 && std::is_same_v<T, bf16_t>) {
+                  if (d2) {
+                    hipLaunchKernelGGL((k_read_d2<SIHC_RD2_U, BB, NT>), dim3(blocks1d(sh.slices, chunks)),
+                                       dim3(sh.bcg, sh.tl), lds, st, static_cast<const T*>(x),
+                                       static_cast<const T*>(alpha), pk, index, events, g, gs, int(chunks),
+                                       sh.slices);
+                    return check_launch(what);
+                  }
+                }
                 if constexpr (((KK == 4 && VV == 2) || (KK == 2 && VV == 8)) && std::is_same_v<T, bf16_t>) {
                   if (wb) return go(std::true_type{});
                 }
@@ -2524,6 +2799,9 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
   const bool wb = w_dtype == SIHC_DTYPE_BF16 &&
                   ((SIHC_K4_BF16W && cell == 4 && V == 2) || (SIHC_K2_BF16W && cell == 2 && V == 8));
   const int wbytes = wb ? 2 : 4;
+  // 16 slots, bf16 carrier, updates and weights, 2-channel lanes: event pairs summed by
+  // dot2 (pair words staged in no more LDS than the packed bf16 weights)
+  const bool d2 = SIHC_K4_DOT2 && wb && cell == 4 && x_dtype == SIHC_DTYPE_BF16;
   const Shape2D sh = cell == 2 ? shape_for(channels, V, SIHC_RW_BCG, E4 * S * wbytes)
                                : shape_for(channels, V, SIHC_RW_BCG_K4, E4 * S * wbytes, SIHC_RW_LDS_K4);
   const int tpb = sh.tl * rw_tokens_per_lane(cell, E4);
@@ -2560,6 +2838,15 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
                                        int(chunks), sh.slices);
                     return check_launch(what);
                   };
+                  if constexpr (KK == 4 && VV == 2 && std::is_same_v<TX, bf16_t> && std::is_same_v<TW, bf16_t>) {
+                    if (d2) {
+                      hipLaunchKernelGGL((k_write_d2<SIHC_WR2_U, AX, BB, NT>), dim3(blocks1d(sh.slices, chunks)),
+                                         dim3(sh.bcg, sh.tl), lds, st, static_cast<const TX*>(x), pk,
+                                         static_cast<const TW*>(beta), static_cast<TX*>(out), index, events, g, gs,
+                                         int(chunks), sh.slices);
+                      return check_launch(what);
+                    }
+                  }
                   if constexpr (((KK == 4 && VV == 2) || (KK == 2 && VV == 8)) && std::is_same_v<TW, bf16_t>) {
                     if (wb) return go(std::true_type{});
                   }
