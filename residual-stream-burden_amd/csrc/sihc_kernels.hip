@@ -1582,6 +1582,147 @@ __global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgradz(const bf16_t* __
 }
 
 // ----------------------------------------------------------------------------------
+// 16-slot bf16 weight gradient with dot2 over token pairs: dW[e,s,c] partials =
+// sum_m z_e[m,c] * x[m,s,c], two tokens per instruction. The block, its event waves and
+// the double-buffered staging follow k_wgradz, but the LDS tiles interleave token pairs:
+// xt2[((tp * 16 + s) * 64 + cl)] holds x[t0 + 2tp, s, cs + cl] | x[t0 + 2tp + 1, s, cs + cl]
+// << 16, zt2[(tp * E + e) * 64 + cl] the same for z_e (a zero high half for the odd last
+// token of a tile). A thread stages both tokens of a pair (two 16-byte loads) and packs
+// them with pair_lo / pair_hi into two 16-byte LDS writes; a lane then reads one word per
+// (pair, slot) and per (pair, event) and issues 16 x EPL dot2 per token pair where
+// k_wgradz issues 32 x EPL FMAs plus the bf16 -> fp32 conversions of 2 x (16 + EPL)
+// 2-byte LDS reads. Partial rows as k_wgradz (the summation order differs: pairs).
+// NPQ: token-pair carrier vectors per thread; EPL: events per wave (lane).
+// ----------------------------------------------------------------------------------
+template <int NPQ, int EPL>
+__global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgradz_d2(const bf16_t* __restrict__ x, PtrPack z,
+                                                                   float* __restrict__ part,
+                                                                   const int32_t* __restrict__ index, int E, Geo g,
+                                                                   int tpb, int nslices) {
+  constexpr bool NTL = true;
+  constexpr int K = 4, S = 16, TT = SIHC_C16Z_TT, VS = 8, NV = C16_LANES / VS;
+  constexpr int TP = TT / 2;           // token pairs per tile
+  constexpr int NXP = TP * S * NV;     // carrier vector pairs per tile
+  constexpr int NZK = (EPL + 1) / 2;   // update events staged per lane (two lane halves)
+  static_assert(TT % 2 == 0 && TP * NV == C16_LANES / 2, "half a wave stages one event's token pairs");
+  using R = u32x4;
+  extern __shared__ __align__(16) unsigned char smem16[];
+  uint32_t* xt = reinterpret_cast<uint32_t*>(smem16);  // [TP][S][64] pair words
+  uint32_t* zt = xt + TP * S * C16_LANES;              // [TP][E][64] pair words
+  const int lane = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.y);
+  const int nw = blockDim.y, nthr = C16_LANES * nw, tid = wave * C16_LANES + lane;
+  const int e0 = wave * EPL;
+  const int blk = logical_block<false>(), slice = blk % nslices, chunk = blk / nslices;
+  const int cs = slice * C16_LANES, c = cs + lane;
+  const bool cok = c < g.C;
+  // this lane's update staging slot: lane half h (events k = h, h + 2, ... of the wave's
+  // share wave + k * nw), token pair zp, vector zj of the 64-channel row
+  const int zh = lane / (C16_LANES / 2), zp = (lane % (C16_LANES / 2)) / NV, zj = lane % NV;
+  const int zc = cs + zj * VS;
+  R xb[NPQ][2], zb[NZK][2];
+  // every load is issued at a clamped in-range address (commit drops what is not part of
+  // the tile), so no branch separates the loads
+  auto issue = [&](int t0, int tn) {
+    int64_t off[NPQ][2];
+#pragma unroll
+    for (int k = 0; k < NPQ; ++k) {
+      const int i = min(tid + k * nthr, NXP - 1);
+      const int row = i / NV, tp = row / S, cc = cs + (i % NV) * VS;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        off[k][h] = slot_offset<K>(cell_pixel0(t0 + min(2 * tp + h, tn - 1), g, index), row % S, g,
+                                   cc < g.C ? cc : cs);
+    }
+    int64_t zoff[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) zoff[h] = int64_t(t0 + min(2 * zp + h, tn - 1)) * g.C + (zc < g.C ? zc : cs);
+#pragma unroll
+    for (int k = 0; k < NPQ; ++k)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) xb[k][h] = ld<NTL>(reinterpret_cast<const R*>(x + off[k][h]));
+#pragma unroll
+    for (int k = 0; k < NZK; ++k) {
+      const int e = min(wave + (2 * k + zh) * nw, E - 1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        zb[k][h] = ld<NTL>(reinterpret_cast<const R*>(static_cast<const bf16_t*>(z.p[e]) + zoff[h]));
+    }
+  };
+  // two 16-byte vectors of 8 channels (tokens 2tp, 2tp + 1) -> 8 pair words in channel order
+  auto put_pairs = [](uint32_t* dst, const R& a, const R& b, bool second) {
+    // word k of a vector holds channels 2k, 2k + 1: pair words 2k = pair_lo, 2k + 1 =
+    // pair_hi; words 0..1 of the vectors give channels 0..3 (lo), words 2..3 channels 4..7
+    R lo, hi;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t bl = second ? b[k] : 0u, bh = second ? b[k + 2] : 0u;
+      lo[2 * k] = pair_lo(a[k], bl);
+      lo[2 * k + 1] = pair_hi(a[k], bl);
+      hi[2 * k] = pair_lo(a[k + 2], bh);
+      hi[2 * k + 1] = pair_hi(a[k + 2], bh);
+    }
+    reinterpret_cast<R*>(dst)[0] = lo;
+    reinterpret_cast<R*>(dst)[1] = hi;
+  };
+  auto commit = [&](int tn) {
+#pragma unroll
+    for (int k = 0; k < NPQ; ++k) {
+      const int i = tid + k * nthr;
+      const int row = i / NV, tp = row / S, j = i % NV, cc = cs + j * VS;
+      if (i < NXP && 2 * tp < tn && cc < g.C) put_pairs(xt + row * C16_LANES + j * VS, xb[k][0], xb[k][1], 2 * tp + 1 < tn);
+    }
+#pragma unroll
+    for (int k = 0; k < NZK; ++k) {
+      const int e = wave + (2 * k + zh) * nw;
+      if (2 * k + zh < EPL && e < E && 2 * zp < tn && zc < g.C)
+        put_pairs(zt + (zp * E + e) * C16_LANES + zj * VS, zb[k][0], zb[k][1], 2 * zp + 1 < tn);
+    }
+  };
+  int zrow[EPL];  // this lane's event rows within a token pair's update rows (clamped)
+#pragma unroll
+  for (int q = 0; q < EPL; ++q) zrow[q] = min(e0 + q, E - 1);
+  float acc[EPL][S];
+#pragma unroll
+  for (int q = 0; q < EPL; ++q)
+#pragma unroll
+    for (int s = 0; s < S; ++s) acc[q][s] = 0.f;
+  const int m_begin = chunk * tpb;
+  const int m_end = min(m_begin + tpb, g.M);
+  if (m_begin < m_end) issue(m_begin, min(TT, m_end - m_begin));
+  for (int t0 = m_begin; t0 < m_end; t0 += TT) {
+    const int tn = min(TT, m_end - t0);
+    __syncthreads();  // the previous tile is fully reduced
+    commit(tn);
+    __syncthreads();
+    if (t0 + TT < m_end) issue(t0 + TT, min(TT, m_end - t0 - TT));
+    load_fence();
+    if (cok) {
+      for (int tp = 0; 2 * tp < tn; ++tp) {
+        uint32_t zv[EPL];
+#pragma unroll
+        for (int q = 0; q < EPL; ++q) zv[q] = zt[(tp * E + zrow[q]) * C16_LANES + lane];
+#pragma unroll
+        for (int sl = 0; sl < S; ++sl) {
+          const uint32_t xs = xt[(tp * S + sl) * C16_LANES + lane];
+#pragma unroll
+          for (int q = 0; q < EPL; ++q) acc[q][sl] = dot2(xs, zv[q], acc[q][sl]);
+        }
+      }
+    }
+  }
+  if (!cok) return;
+#pragma unroll
+  for (int q = 0; q < EPL; ++q) {
+    if (e0 + q < E) {
+      float* prow = part + (int64_t(chunk) * E + e0 + q) * S * g.C + c;
+#pragma unroll
+      for (int sl = 0; sl < S; ++sl) prow[int64_t(sl) * g.C] = acc[q][sl];
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------
 // Fixed-order sum of partial rows. part is [chunks][R][S][C]; row r of the result
 // goes to out0 + r*C*S ([R][C][S], `pair` == 0) or, with `pair`, row 0 -> out0 and
 // row 1 -> out1 (each [C][S]). Rows whose bit is set in zero_mask are written as
@@ -2545,12 +2686,26 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
             constexpr int NQ = decltype(nq)::value;
             constexpr int EP = decltype(ep)::value;
             const size_t ldsz = size_t(SIHC_C16Z_TT) * (KZ * KZ + events) * C16_LANES * sizeof(bf16_t);
+            // 16 slots: token pairs summed by dot2 (the same LDS bytes, NQ / 2 vector pairs
+            // per thread)
+            constexpr int NPQ = (NQ + 1) / 2;
+            constexpr bool D2 = SIHC_K4_DOT2 && KZ == 4;
+            const void* kfn;
+            if constexpr (D2) {
+              kfn = reinterpret_cast<const void*>(&k_wgradz_d2<NPQ, EP>);
+            } else {
+              kfn = reinterpret_cast<const void*>(&k_wgradz<KZ, NQ, EP>);
+            }
             // whole rounds of resident blocks, so the last round is not part-empty
-            const void* kfn = reinterpret_cast<const void*>(&k_wgradz<KZ, NQ, EP>);
             chunks = whole_rounds(slicesz, max_chunks, resident_blocks(kfn, C16_LANES * nw, ldsz));
             const int tpbz = int((int64_t(g.M) + chunks - 1) / chunks);
-            hipLaunchKernelGGL((k_wgradz<KZ, NQ, EP>), dim3(blocks1d(slicesz, chunks)), dim3(C16_LANES, nw), ldsz, st,
-                               reinterpret_cast<const bf16_t*>(x), pk, part, index, events, g, tpbz, slicesz);
+            if constexpr (D2) {
+              hipLaunchKernelGGL((k_wgradz_d2<NPQ, EP>), dim3(blocks1d(slicesz, chunks)), dim3(C16_LANES, nw), ldsz,
+                                 st, reinterpret_cast<const bf16_t*>(x), pk, part, index, events, g, tpbz, slicesz);
+            } else {
+              hipLaunchKernelGGL((k_wgradz<KZ, NQ, EP>), dim3(blocks1d(slicesz, chunks)), dim3(C16_LANES, nw), ldsz,
+                                 st, reinterpret_cast<const bf16_t*>(x), pk, part, index, events, g, tpbz, slicesz);
+            }
           };
           // events per lane: the first candidate giving 4 or 8 event waves (0: none)
           auto balanced_epl = [&](std::initializer_list<int> cands) {
