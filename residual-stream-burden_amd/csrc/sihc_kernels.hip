@@ -57,6 +57,12 @@
 #ifndef SIHC_EV_UNROLL  // tokens per lane per loop iteration, per-event kernels
 #define SIHC_EV_UNROLL 2
 #endif
+#ifndef SIHC_EV_BWD16  // 1: 16-slot bf16 per-event backward on the register-lean kernel
+#define SIHC_EV_BWD16 1
+#endif
+#ifndef SIHC_EV16_MINW  // occupancy hint (min waves per SIMD) of the 16-slot per-event backward
+#define SIHC_EV16_MINW 2
+#endif
 #ifndef SIHC_EV_MINW  // occupancy hint (min waves per SIMD) of the per-event kernels
 #define SIHC_EV_MINW 1
 #endif
@@ -2097,6 +2103,146 @@ __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_bwd(const T* __rest
 }
 
 // ----------------------------------------------------------------------------------
+// 16-slot bf16 per-event backward with 2-channel lanes: k_event_bwd's arithmetic in the
+// same order (so the same bits), one token per lane per iteration, and the weights and
+// loaded rows kept as bf16 words, widened where they are used. A lane's 16-slot cell
+// otherwise holds 68 loaded values per token beside 64 accumulators and 64 weights:
+// k_event_bwd at 16 slots needs 334 VGPRs with two tokens per lane (one wave per SIMD).
+// A lane reads its channel pair's 16-slot weight rows ([C][16] bf16: 8 words per channel,
+// word p = slots 2p, 2p + 1) with four 16-byte loads. The token order per thread equals
+// k_event_bwd's (tokens ty, ty + TL, ... of each group), so the partial rows are the same.
+// ----------------------------------------------------------------------------------
+template <bool HAS_H, bool HAS_G, bool HAS_W, bool STORE_T, bool NTL, bool NTS>
+__global__ void __launch_bounds__(256, SIHC_EV16_MINW) k_event_bwd16(const bf16_t* __restrict__ gxo,
+                                                     const bf16_t* __restrict__ gzo,
+                                                     const bf16_t* __restrict__ xo, const bf16_t* __restrict__ dz,
+                                                     const bf16_t* __restrict__ beta,
+                                                     const bf16_t* __restrict__ alpha, bf16_t* __restrict__ gx,
+                                                     bf16_t* __restrict__ gdz, float* __restrict__ part,
+                                                     const int32_t* __restrict__ index, Geo g, int gs, int nchunks,
+                                                     int nslices) {
+  constexpr int K = 4, S = 16, V = 2;
+  extern __shared__ float red[];
+  const int BCG = blockDim.x, TL = blockDim.y;
+  const int BC = BCG * V;
+  const int blk = logical_block<true>(), slice = blk % nslices, chunk = blk / nslices;
+  const int c0 = slice * BC + threadIdx.x * V;
+  float db[S][V], da[S][V];
+#pragma unroll
+  for (int sl = 0; sl < S; ++sl)
+#pragma unroll
+    for (int v = 0; v < V; ++v) db[sl][v] = da[sl][v] = 0.f;
+  // word w of a weight row pair: channel w / 8, slots 2 (w % 8), 2 (w % 8) + 1
+  auto wget = [](const uint32_t (&w)[16], int sl, int v) {
+    const uint32_t u = w[v * 8 + (sl >> 1)];
+    return __uint_as_float((sl & 1) ? (u & 0xffff0000u) : (u << 16));
+  };
+  auto lo_f = [](uint32_t u) { return __uint_as_float(u << 16); };
+  auto hi_f = [](uint32_t u) { return __uint_as_float(u & 0xffff0000u); };
+  if (c0 < g.C) {
+    uint32_t bw[16], aw[16];
+    if constexpr (HAS_W) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x4 r = reinterpret_cast<const u32x4*>(beta + int64_t(c0) * S)[q];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bw[4 * q + k] = r[k];
+      }
+    }
+    if constexpr (HAS_G) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x4 r = reinterpret_cast<const u32x4*>(alpha + int64_t(c0) * S)[q];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) aw[4 * q + k] = r[k];
+      }
+    }
+    const int64_t M = g.M;
+    const int64_t row_w = int64_t(g.GK) * (g.C >> 1);  // words per carrier row (C even here)
+    const int pix_w = g.C >> 1;
+    const uint32_t* gxw = reinterpret_cast<const uint32_t*>(gxo);
+    const uint32_t* xow = reinterpret_cast<const uint32_t*>(xo);
+    uint32_t* gxo_w = reinterpret_cast<uint32_t*>(gx);
+    for (int64_t m0 = int64_t(chunk) * gs; m0 < M; m0 += int64_t(nchunks) * gs) {
+      const int64_t m_end = min(m0 + gs, M);
+      for (int64_t mi = m0; mi < m_end; mi += TL) {
+        const int64_t mt = mi + threadIdx.y;
+        const bool ok = mt < m_end;
+        const int mu = int(ok ? mt : mi);  // tail: reload the iteration's first token
+        const int64_t b0 = (cell_pixel0(mu, g, index) * g.C + c0) >> 1;
+        const int64_t zw = (int64_t(mu) * g.C + c0) >> 1;
+        uint32_t gzr = 0u, dr = 0u, tr[S], xr[S];
+        if constexpr (HAS_G) gzr = ld<NTL>(reinterpret_cast<const uint32_t*>(gzo) + zw);
+        if constexpr (HAS_W) dr = ld<NTL>(reinterpret_cast<const uint32_t*>(dz) + zw);
+#pragma unroll
+        for (int uy = 0; uy < K; ++uy)
+#pragma unroll
+          for (int ux = 0; ux < K; ++ux) {
+            const int64_t o = b0 + uy * row_w + ux * pix_w;
+            tr[uy * K + ux] = HAS_H ? ld<NTL>(gxw + o) : 0u;
+            if constexpr (HAS_G) xr[uy * K + ux] = ld<NTL>(xow + o);
+          }
+        load_fence();
+        // a tail token adds exactly nothing: every loaded value is zeroed (a zero factor
+        // alone would turn an Inf in the repeated token into NaN), and nothing is stored
+        if (!ok) {
+          gzr = dr = 0u;
+#pragma unroll
+          for (int sl = 0; sl < S; ++sl) tr[sl] = xr[sl] = 0u;
+        }
+        const float gz[V] = {lo_f(gzr), hi_f(gzr)}, d[V] = {lo_f(dr), hi_f(dr)};
+        float gd[V] = {0.f, 0.f};
+#pragma unroll
+        for (int sl = 0; sl < S; ++sl) {
+          float t[V] = {lo_f(tr[sl]), hi_f(tr[sl])};
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            if constexpr (HAS_G) {
+              const float xv = v ? hi_f(xr[sl]) : lo_f(xr[sl]);
+              da[sl][v] = fmaf(xv, gz[v], da[sl][v]);
+              t[v] = fmaf(wget(aw, sl, v), gz[v], t[v]);
+            }
+            if constexpr (HAS_W) {
+              gd[v] = fmaf(wget(bw, sl, v), t[v], gd[v]);
+              db[sl][v] = fmaf(d[v], t[v], db[sl][v]);
+            }
+          }
+          if constexpr (STORE_T) {
+            if (ok) {
+              const int uy = sl / K, ux = sl % K;
+              store_vec<bf16_t, V, NTS>(reinterpret_cast<bf16_t*>(gxo_w + b0 + uy * row_w + ux * pix_w), t);
+            }
+          }
+        }
+        if constexpr (HAS_W) {
+          if (ok) store_vec<bf16_t, V, NTS>(gdz + (int64_t(mu) * g.C + c0), gd);
+        }
+      }
+    }
+  }
+  // Block reduction of the [S][V] accumulators, as k_event_bwd: partial rows [2][S][C].
+  float* prow = part + int64_t(chunk) * 2 * S * g.C;
+  const int cs = slice * BC;
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    if ((w == 0 && !HAS_W) || (w == 1 && !HAS_G)) continue;
+    float flat[S * V];
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl)
+#pragma unroll
+      for (int v = 0; v < V; ++v) flat[sl * V + v] = w == 0 ? db[sl][v] : da[sl][v];
+    block_reduce_rows<S * V>(flat, red, [&](int i, float sum) {
+      const int lane = i / (S * V);
+      const int r = i - lane * S * V;
+      const int sl = r / V;
+      const int v = r - sl * V;
+      const int c = cs + lane * V + v;
+      if (c < g.C) prow[(int64_t(w) * S + sl) * g.C + c] = sum;
+    });
+  }
+}
+
+// ----------------------------------------------------------------------------------
 // gather / scatter of whole cells (bit-exact copies of CH-byte chunks)
 // cells[m][s][:] <-> x[pixel(index(m), s)][:]
 // ----------------------------------------------------------------------------------
@@ -3268,12 +3414,28 @@ static int event_backward_impl(const char* what, const void* grad_x_out, const v
             auto go = [&](auto hg, auto hw, auto stt) {
               constexpr bool HG = decltype(hg)::value, HW = decltype(hw)::value, STT = decltype(stt)::value;
               constexpr bool NTL = (SIHC_EV_BWD_NT & 1) != 0, NTS = (SIHC_EV_BWD_NT & 2) != 0;
-              const void* kfn = reinterpret_cast<const void*>(&k_event_bwd<T, VV, KK, HH, HG, HW, STT, NTL, NTS>);
+              // 16-slot bf16 cells with 2-channel lanes: the register-lean kernel
+              constexpr bool B16 = SIHC_EV_BWD16 && KK == 4 && VV == 2 && std::is_same_v<T, bf16_t>;
+              const void* kfn;
+              if constexpr (B16) {
+                kfn = reinterpret_cast<const void*>(&k_event_bwd16<HH, HG, HW, STT, NTL, NTS>);
+              } else {
+                kfn = reinterpret_cast<const void*>(&k_event_bwd<T, VV, KK, HH, HG, HW, STT, NTL, NTS>);
+              }
               chunks = whole_rounds(sh.slices, max_chunks, resident_blocks(kfn, sh.bcg * sh.tl, lds));
               // token groups: a multiple of one loop iteration (SIHC_EV_UNROLL x TL tokens);
               // group 0 means one contiguous run of tokens per chunk
               const int gs = group_tokens(KK == 2 ? SIHC_EV_GROUP : SIHC_EV_GROUP_K4, g.M, chunks,
                                           SIHC_EV_UNROLL * sh.tl);
+              if constexpr (B16) {
+                hipLaunchKernelGGL((k_event_bwd16<HH, HG, HW, STT, NTL, NTS>), dim3(blocks1d(sh.slices, chunks)),
+                                   dim3(sh.bcg, sh.tl), lds, st, static_cast<const T*>(grad_x_out),
+                                   static_cast<const T*>(grad_z_out), static_cast<const T*>(x_out),
+                                   static_cast<const T*>(dz), static_cast<const T*>(beta),
+                                   static_cast<const T*>(alpha_next), static_cast<T*>(grad_x),
+                                   static_cast<T*>(grad_dz), part, index, g, gs, chunks, sh.slices);
+                return check_launch(what);
+              }
               hipLaunchKernelGGL((k_event_bwd<T, VV, KK, HH, HG, HW, STT, NTL, NTS>), dim3(blocks1d(sh.slices, chunks)),
                                  dim3(sh.bcg, sh.tl), lds, st, static_cast<const T*>(grad_x_out),
                                  static_cast<const T*>(grad_z_out), static_cast<const T*>(x_out),
