@@ -57,6 +57,9 @@
 #ifndef SIHC_EV_UNROLL  // tokens per lane per loop iteration, per-event kernels
 #define SIHC_EV_UNROLL 2
 #endif
+#ifndef SIHC_EV_FWD16  // 1: 16-slot bf16 per-event forward on the register-lean kernel
+#define SIHC_EV_FWD16 1
+#endif
 #ifndef SIHC_EV_BWD16  // 1: 16-slot bf16 per-event backward on the register-lean kernel
 #define SIHC_EV_BWD16 1
 #endif
@@ -1966,6 +1969,89 @@ __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_fwd(const T* __rest
 }
 
 // ----------------------------------------------------------------------------------
+// 16-slot bf16 per-event forward with 2-channel lanes: k_event_fwd's arithmetic (same
+// bits), with the carrier rows and the weights kept as bf16 words and each slot widened,
+// updated, rounded and stored in turn (k_event_fwd holds 2 x 16 x 2 fp32 carrier values
+// and 64 fp32 weights per lane at 16 slots: 145 VGPRs, 3 waves per SIMD).
+// ----------------------------------------------------------------------------------
+template <bool HAS_Z, bool NTL, bool NTS>
+__global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_fwd16(const bf16_t* __restrict__ x,
+                                                     const bf16_t* __restrict__ dz,
+                                                     const bf16_t* __restrict__ beta,
+                                                     const bf16_t* __restrict__ alpha, bf16_t* __restrict__ xo,
+                                                     bf16_t* __restrict__ zo, const int32_t* __restrict__ index,
+                                                     Geo g, int tpb, int nslices) {
+  constexpr int K = 4, S = 16, V = 2;
+  constexpr int U = SIHC_EV_UNROLL;  // tokens per lane per iteration
+  const int BCG = blockDim.x, TL = blockDim.y;
+  const int blk = logical_block<true>(), slice = blk % nslices, chunk = blk / nslices;
+  const int c0 = (slice * BCG + threadIdx.x) * V;
+  if (c0 >= g.C) return;
+  uint32_t bw[16], aw[16];  // word v * 8 + p: channel c0 + v, slots 2p, 2p + 1
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const u32x4 r = reinterpret_cast<const u32x4*>(beta + int64_t(c0) * S)[q];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) bw[4 * q + k] = r[k];
+  }
+  if constexpr (HAS_Z) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x4 r = reinterpret_cast<const u32x4*>(alpha + int64_t(c0) * S)[q];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) aw[4 * q + k] = r[k];
+    }
+  }
+  auto wget = [](const uint32_t (&w)[16], int sl, int v) {
+    const uint32_t u = w[v * 8 + (sl >> 1)];
+    return __uint_as_float((sl & 1) ? (u & 0xffff0000u) : (u << 16));
+  };
+  const int64_t row_w = int64_t(g.GK) * (g.C >> 1);  // words per carrier row (C even here)
+  const int pix_w = g.C >> 1;
+  const uint32_t* xw = reinterpret_cast<const uint32_t*>(x);
+  uint32_t* xow = reinterpret_cast<uint32_t*>(xo);
+  const int m_begin = chunk * tpb;
+  const int m_end = min(m_begin + tpb, g.M);
+  for (int m = m_begin + threadIdx.y; m < m_end; m += U * TL) {
+    int64_t b0[U], zw[U];
+    bool ok[U];
+    uint32_t dr[U], xr[U][S];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      ok[u] = m + u * TL < m_end;
+      const int mu = ok[u] ? m + u * TL : m;  // tail: reload a valid token, store nothing
+      b0[u] = (cell_pixel0(mu, g, index) * g.C + c0) >> 1;
+      zw[u] = (int64_t(mu) * g.C + c0) >> 1;
+      dr[u] = ld<NTL>(reinterpret_cast<const uint32_t*>(dz) + zw[u]);
+#pragma unroll
+      for (int uy = 0; uy < K; ++uy)
+#pragma unroll
+        for (int ux = 0; ux < K; ++ux) xr[u][uy * K + ux] = ld<NTL>(xw + b0[u] + uy * row_w + ux * pix_w);
+    }
+    load_fence();
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float d[V] = {__uint_as_float(dr[u] << 16), __uint_as_float(dr[u] & 0xffff0000u)};
+      float zacc[V] = {0.f, 0.f};
+#pragma unroll
+      for (int sl = 0; sl < S; ++sl) {
+        float xv[V] = {__uint_as_float(xr[u][sl] << 16), __uint_as_float(xr[u][sl] & 0xffff0000u)};
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          xv[v] = round_as<bf16_t>(fmaf(wget(bw, sl, v), d[v], xv[v]));
+          if constexpr (HAS_Z) zacc[v] = fmaf(wget(aw, sl, v), xv[v], zacc[v]);
+        }
+        if (ok[u])
+          store_vec<bf16_t, V, NTS>(reinterpret_cast<bf16_t*>(xow + b0[u] + (sl / K) * row_w + (sl % K) * pix_w), xv);
+      }
+      if constexpr (HAS_Z) {
+        if (ok[u]) store_vec<bf16_t, V, NTS>(zo + 2 * zw[u], zacc);
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------
 // per-event fused backward (see sihc_event_backward in sihc_hip.h)
 //   HAS_H: grad_x_out given      HAS_G: read part (grad_z_out, x_out, alpha_next)
 //   HAS_W: write part (dz, beta)  STORE_T: store t as grad_x (else the caller aliases)
@@ -3329,6 +3415,13 @@ int sihc_event_forward(const void* x, const void* dz, const void* beta, const vo
           return with_bool(alpha_next != nullptr, [&](auto hz) {
             constexpr bool HZ = decltype(hz)::value;
             constexpr bool NTL = (SIHC_EV_FWD_NT & 1) != 0, NTS = (SIHC_EV_FWD_NT & 2) != 0;
+            if constexpr (SIHC_EV_FWD16 && KK == 4 && VV == 2 && std::is_same_v<T, bf16_t>) {
+              hipLaunchKernelGGL((k_event_fwd16<HZ, NTL, NTS>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl),
+                                 0, st, static_cast<const T*>(x), static_cast<const T*>(dz),
+                                 static_cast<const T*>(beta), static_cast<const T*>(alpha_next),
+                                 static_cast<T*>(x_out), static_cast<T*>(z_out), index, g, tpb, sh.slices);
+              return check_launch(what);
+            }
             hipLaunchKernelGGL((k_event_fwd<T, VV, KK, HZ, NTL, NTS>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), 0,
                                st, static_cast<const T*>(x), static_cast<const T*>(dz), static_cast<const T*>(beta),
                                static_cast<const T*>(alpha_next), static_cast<T*>(x_out), static_cast<T*>(z_out),

@@ -511,3 +511,59 @@ def run_bwd16(B, G, C, parts, index=False, chunks=None, seed=0):
     err = max((np.max(np.abs(P[w] - rP[w])) / max(np.max(np.abs(rP[w])), 1e-30)) for w in rows) if rows else 0.0
     assert err < 1e-5, err
     print(f"event_bwd16 B={B} G={G} C={C} parts={parts} index={index} chunks={chunks}: bounds ok, outputs within 1 ulp, partial sums rel err {err:.1e}", flush=True)
+
+def emu_event_fwd16(x, dz, beta, alpha, g, index, has_z=True, U=2, TPT=2):
+    K, S, V, C, M = 4, 16, 2, g.C, g.M
+    bcg, tl, slices = shape_for(C, 2, 32, 0)
+    tpb = tl * TPT; chunks = -(-M // tpb); n = slices * chunks
+    xw = Arr(len(x) // 2, "x", data=x.view(np.uint32)); dzw = Arr(M * C // 2, "dz", data=dz.view(np.uint32))
+    bw16 = Arr(len(beta) // 2, "beta", data=beta.view(np.uint32)); aw16 = Arr(len(alpha) // 2, "alpha", data=alpha.view(np.uint32))
+    xo = Arr(len(x) // 2, "xo"); zo = Arr(M * C, "zo", dtype=np.uint16)
+    row_w = g.GK * (C >> 1); pix_w = C >> 1
+    wget = lambda w, s_, v: bf((int(w[v * 8 + (s_ >> 1)]) >> 16) if (s_ & 1) else (int(w[v * 8 + (s_ >> 1)]) & 0xFFFF))
+    for b in range(n):
+        blk = logical_block(b, n, True); sl_ = blk % slices; chunk = blk // slices
+        for ty in range(tl):
+            for tx in range(bcg):
+                c0 = (sl_ * bcg + tx) * V
+                if c0 >= C: continue
+                bwv = [bw16[(c0 * S) // 2 + k] for k in range(16)]
+                awv = [aw16[(c0 * S) // 2 + k] for k in range(16)] if has_z else None
+                m_begin = chunk * tpb; m_end = min(m_begin + tpb, M)
+                for m in range(m_begin + ty, m_end, U * tl):
+                    for u in range(U):
+                        ok = m + u * tl < m_end; mu = m + u * tl if ok else m
+                        p = cell_pixel0(mu, g, index) * C + c0; b0 = p >> 1; zwi = (mu * C + c0) >> 1
+                        dr = int(dzw[zwi]); d = [bf(dr & 0xFFFF), bf(dr >> 16)]
+                        zacc = [np.float32(0), np.float32(0)]
+                        for s_ in range(S):
+                            o = b0 + (s_ // K) * row_w + (s_ % K) * pix_w
+                            xr = int(xw[o]); xv = [bf(xr & 0xFFFF), bf(xr >> 16)]
+                            for v in range(V):
+                                xv[v] = bf(bf16_bits(np.float32(float(wget(bwv, s_, v)) * float(d[v]) + float(xv[v]))))
+                                if has_z: zacc[v] = np.float32(float(wget(awv, s_, v)) * float(xv[v]) + float(zacc[v]))
+                            if ok:
+                                bits = bf16_bits(np.array(xv, np.float32)); xo[o] = int(bits[0]) | (int(bits[1]) << 16)
+                        if has_z and ok:
+                            bits = bf16_bits(np.array(zacc, np.float32)); zo[2 * zwi] = bits[0]; zo[2 * zwi + 1] = bits[1]
+    return xo.a, zo.a
+
+def run_fwd16(B, G, C, index=False, seed=0):
+    rng = np.random.default_rng(seed)
+    g = Geo(B, G, 4, C)
+    idx = np.array([(m % g.GG * 7 + 3) % g.GG for m in range(g.M)], np.int32) if index else None
+    x = bf16_bits(rng.standard_normal(B * g.GK * g.GK * C)); dz = bf16_bits(rng.standard_normal(g.M * C))
+    beta = bf16_bits(1 + 0.02 * rng.standard_normal(C * 16)); alpha = bf16_bits(0.25 + 0.02 * rng.standard_normal(C * 16))
+    xo, zo = emu_event_fwd16(x, dz, beta, alpha, g, idx)
+    X = bf(x).astype(np.float64); D = bf(dz).astype(np.float64).reshape(g.M, C)
+    b = bf(beta).astype(np.float64).reshape(C, 16); a = bf(alpha).astype(np.float64).reshape(C, 16)
+    rx = X.copy(); rz = np.zeros((g.M, C))
+    for m in range(g.M):
+        p0 = cell_pixel0(m, g, idx)
+        for s in range(16):
+            o = slot_offset(p0, s, g, 0)
+            v = bf(bf16_bits((X[o:o + C] + b[:, s] * D[m]).astype(np.float32))).astype(np.float64)
+            rx[o:o + C] = v; rz[m] += a[:, s] * v
+    e1 = ulps_ok(xo.view(np.uint16), rx); e2 = ulps_ok(zo, rz.reshape(-1))
+    assert e1 <= 1.0 and e2 <= 1.0, (e1, e2)
+    print(f"event_fwd16 B={B} G={G} C={C} index={index}: bounds ok, x_out {e1:.2f} ulp, z_out {e2:.2f} ulp", flush=True)
