@@ -1255,6 +1255,14 @@ __global__ void __launch_bounds__(256, SIHC_TRIB_MINB) k_trib_waves(const T* __r
       const int e = wave + k * NW;
       if (e < E) emit(acc[k], e);
     }
+  } else if (m_begin >= m_end) {
+    // a chunk past the last token (chunks x tpb can exceed M by more than tpb) still owns
+    // its partial rows: zeros, so the finalize never reads rows nobody wrote
+#pragma unroll
+    for (int k = 0; k < TRIB_MAXK; ++k) {
+      const int e = wave + k * NW;
+      if (e < E) emit(acc[0], e);
+    }
   }
 }
 
