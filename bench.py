@@ -255,33 +255,57 @@ class LiteralStep:
                                          vp(self.galpha[0].data_ptr()), Bh, G, K, C, None)))
             halves.append(calls)
         self.halves = halves
-        self.finalize2_args = None
 
-    def step2(self):
-        """One fwd+bwd step as two half-batch streams, then the deferred finalize of both
-        halves' partial rows on the launch stream."""
-        torch = self.torch
-        main = torch.cuda.current_stream()
-        for st in self.streams2:
-            st.wait_stream(main)
-        for a, b in zip(*self.halves):  # interleaved enqueue: both streams get work early
-            self.check(a())
-            self.check(b())
-        for st in self.streams2:
-            main.wait_stream(st)
+    def _finalize2(self, slots, stream):
+        """sihc_event_finalize of the listed deferred slots (both halves' partial rows)."""
         E = self.E
-        for k in range(E + 1):
+        for k in slots:
             c0, r0 = self.info_h[0][2 * k], self.info_h[0][2 * k + 1]
             c1, r1 = self.info_h[1][2 * k], self.info_h[1][2 * k + 1]
             assert r0 == r1, "the halves ran different parts"
             self.info2[2 * k], self.info2[2 * k + 1] = c0 + c1, r0
-        if self.finalize2_args is None:
+        key = tuple(slots)
+        if key not in self.finalize2_args:
+            gb = [self.gbeta[i] for i in range(E)] + [None]
+            ga = [self.galpha[i + 1] for i in range(E - 1)] + [None, self.galpha[0]]
             ptrs = lambda ts: (ctypes.c_void_p * len(ts))(*(None if t is None else t.data_ptr() for t in ts))  # noqa
-            self.finalize2_args = (E + 1, ptrs(self.work2), self.info2,
-                                   ptrs([self.gbeta[i] for i in range(E)] + [None]),
-                                   ptrs([self.galpha[i + 1] for i in range(E - 1)] + [None, self.galpha[0]]),
-                                   self.K, self.C, 1, self.stream)
-        self.check(self.L.sihc_event_finalize(*self.finalize2_args))
+            info = (ctypes.c_int * (2 * len(slots)))()
+            self.finalize2_args[key] = (info, (len(slots), ptrs([self.work2[k] for k in slots]), info,
+                                               ptrs([gb[k] for k in slots]), ptrs([ga[k] for k in slots]),
+                                               self.K, self.C, 1))
+        info, args = self.finalize2_args[key]
+        for j, k in enumerate(slots):
+            info[2 * j], info[2 * j + 1] = self.info2[2 * k], self.info2[2 * k + 1]
+        self.check(self.L.sihc_event_finalize(*args, ctypes.c_void_p(stream.cuda_stream)))
+
+    def step2(self):
+        """One fwd+bwd step as two half-batch streams. The deferred finalize of the events
+        both halves have passed by the middle of the backward runs on a third stream,
+        overlapping the rest of the backward; the remaining events are finalized on the
+        launch stream after both halves end."""
+        torch = self.torch
+        main = torch.cuda.current_stream()
+        if not hasattr(self, "fin_stream"):
+            self.fin_stream = torch.cuda.Stream(self.x[0].device)
+            self.finalize2_args = {}
+        for st in self.streams2:
+            st.wait_stream(main)
+        E = self.E
+        # call positions: read, E forward events, then the backward of slot E - 1, of slots
+        # E - 2 .. 0, and of slot E (the first read's adjoint)
+        mid_slot = E // 2
+        mid_pos = (E + 1) + (E - 1 - mid_slot)
+        for pos, (a, b) in enumerate(zip(*self.halves)):  # interleaved: both streams get work early
+            self.check(a())
+            self.check(b())
+            if pos == mid_pos:
+                for st in self.streams2:
+                    self.fin_stream.wait_stream(st)
+                self._finalize2(list(range(mid_slot, E)), self.fin_stream)
+        for st in self.streams2:
+            main.wait_stream(st)
+        self._finalize2(list(range(mid_slot)) + [E], main)
+        main.wait_stream(self.fin_stream)
 
     def _finalize(self):
         """sihc_event_finalize over the E + 1 deferred backward calls: slot i < E holds
