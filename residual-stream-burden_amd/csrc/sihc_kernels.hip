@@ -66,6 +66,9 @@
 #ifndef SIHC_EV16_MINW  // occupancy hint (min waves per SIMD) of the 16-slot per-event backward
 #define SIHC_EV16_MINW 2
 #endif
+#ifndef SIHC_EV_FWD_THREADS  // threads per one-shot block of the per-event forward (256 or 512)
+#define SIHC_EV_FWD_THREADS 256
+#endif
 #ifndef SIHC_EV_MINW  // occupancy hint (min waves per SIMD) of the per-event kernels
 #define SIHC_EV_MINW 1
 #endif
@@ -1923,7 +1926,7 @@ __device__ __forceinline__ void load_weights(const T* __restrict__ w, int c0, fl
 }
 
 template <typename T, int V, int K, bool HAS_Z, bool NTL, bool NTS>
-__global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_fwd(const T* __restrict__ x, const T* __restrict__ dz,
+__global__ void __launch_bounds__(SIHC_EV_FWD_THREADS, SIHC_EV_MINW) k_event_fwd(const T* __restrict__ x, const T* __restrict__ dz,
                                                    const T* __restrict__ beta,
                                                    const T* __restrict__ alpha, T* __restrict__ xo,
                                                    T* __restrict__ zo, const int32_t* __restrict__ index,
@@ -1983,7 +1986,7 @@ __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_fwd(const T* __rest
 // and 64 fp32 weights per lane at 16 slots: 145 VGPRs, 3 waves per SIMD).
 // ----------------------------------------------------------------------------------
 template <bool HAS_Z, bool NTL, bool NTS>
-__global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_fwd16(const bf16_t* __restrict__ x,
+__global__ void __launch_bounds__(SIHC_EV_FWD_THREADS, SIHC_EV_MINW) k_event_fwd16(const bf16_t* __restrict__ x,
                                                      const bf16_t* __restrict__ dz,
                                                      const bf16_t* __restrict__ beta,
                                                      const bf16_t* __restrict__ alpha, bf16_t* __restrict__ xo,
@@ -3407,7 +3410,8 @@ int sihc_event_forward(const void* x, const void* dz, const void* beta, const vo
   while (V > 1 && (!aligned(beta, std::min(16, V * S * es)) ||
                    (alpha_next && !aligned(alpha_next, std::min(16, V * S * es)))))
     V /= 2;
-  const Shape2D sh = shape_for(channels, V, SIHC_EV_BCG, 0);
+  Shape2D sh = shape_for(channels, V, SIHC_EV_BCG, 0);
+  sh.tl = SIHC_EV_FWD_THREADS / sh.bcg;  // one-shot blocks of SIHC_EV_FWD_THREADS threads
   const int tpb = sh.tl * SIHC_EV_TPT;
   const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
   hipStream_t st = static_cast<hipStream_t>(stream);
