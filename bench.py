@@ -50,6 +50,8 @@ def parse_args():
     p.add_argument("--seed", type=int, default=2)
     p.add_argument("--streams", type=int, choices=(1, 2), default=1,
                    help="config 2 as one chain, or two half-batch chains on two HIP streams")
+    p.add_argument("--overlap-finalize", action="store_true",
+                   help="one-stream step with half of the deferred finalize on a second stream")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true", help="skip the secondary config 1/3/4 figures")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
@@ -318,6 +320,45 @@ class LiteralStep:
                                   ptrs([self.galpha[i + 1] for i in range(E - 1)] + [None, self.galpha[0]]),
                                   self.K, self.C, 1, self.stream)
         return self.L.sihc_event_finalize(*self.finalize_args)
+
+    def _finalize_slots(self, slots, stream):
+        """sihc_event_finalize of the listed deferred slots of the one-stream step."""
+        E = self.E
+        key = ("one",) + tuple(slots)
+        if not hasattr(self, "fin_args"):
+            self.fin_args = {}
+        if key not in self.fin_args:
+            gb = [self.gbeta[i] for i in range(E)] + [None]
+            ga = [self.galpha[i + 1] for i in range(E - 1)] + [None, self.galpha[0]]
+            ptrs = lambda ts: (ctypes.c_void_p * len(ts))(*(None if t is None else t.data_ptr() for t in ts))  # noqa
+            info = (ctypes.c_int * (2 * len(slots)))()
+            self.fin_args[key] = (info, (len(slots), ptrs([self.work[k] for k in slots]), info,
+                                         ptrs([gb[k] for k in slots]), ptrs([ga[k] for k in slots]), self.K, self.C, 1))
+        info, args = self.fin_args[key]
+        for j, k in enumerate(slots):
+            info[2 * j], info[2 * j + 1] = self.info[2 * k], self.info[2 * k + 1]
+        self.check(self.L.sihc_event_finalize(*args, ctypes.c_void_p(stream.cuda_stream)))
+
+    def step_overlap(self):
+        """The one-stream step with the deferred finalize of the events already passed at
+        the middle of the backward run on a second stream, overlapping the rest of the
+        backward (the remaining events are finalized at the end, as in step())."""
+        torch = self.torch
+        main = torch.cuda.current_stream()
+        if not hasattr(self, "fin_stream1"):
+            self.fin_stream1 = torch.cuda.Stream(self.x[0].device)
+        E = self.E
+        mid_slot = E // 2
+        self.run(self.fwd)
+        body = self.bwd[:-1]  # without the deferred finalize of every event
+        mid_pos = E - 1 - mid_slot  # position of slot mid_slot's call in the backward list
+        for pos, (_, fn, args, _) in enumerate(body):
+            self.check(fn(*args))
+            if pos == mid_pos:
+                self.fin_stream1.wait_stream(main)
+                self._finalize_slots(list(range(mid_slot, E)), self.fin_stream1)
+        self._finalize_slots(list(range(mid_slot)) + [E], main)
+        main.wait_stream(self.fin_stream1)
 
     def run(self, calls):
         for _, fn, args, _ in calls:
@@ -1062,7 +1103,7 @@ def main():
     if two and step.halves is None:
         print("--streams 2 needs an even batch", file=sys.stderr)
         sys.exit(2)
-    run_step = step.step2 if two else step.step
+    run_step = step.step2 if two else (step.step_overlap if args.overlap_finalize else step.step)
     torch.cuda.synchronize()
     for _ in range(args.warmup):
         run_step()
@@ -1084,6 +1125,8 @@ def main():
         a.record()
         if two:
             step.step2()
+        elif args.overlap_finalize:
+            step.step_overlap()
         else:
             step.step(marks)
         c.record()
@@ -1093,7 +1136,7 @@ def main():
     ms_step = wall / args.steps * 1e3
     step_ms = statistics.median(a.elapsed_time(c) for a, c in t_fwd)
     one_stream_ms = None
-    if two:
+    if two or args.overlap_finalize:
         t_one = []
         for _ in range(max(2, min(args.steps, 5))):
             a, c = ev(), ev()

@@ -46,3 +46,16 @@ def test_two_stream_step_matches_one_stream(batch, events):
     for k in ("gbeta", "galpha"):
         assert_parity(two[k], one[k].float(), torch.bfloat16, kind="reduced", what=f"{k} two-stream vs one")
         assert torch.equal(two[k], again[k]), f"{k} not repeatable"
+
+
+def test_overlapped_finalize_is_bit_identical():
+    """The one-stream step whose first finalize batch runs on a second stream: the same
+    partial rows summed by the same kernel, so every output has the same bits."""
+    announce("one-stream step with overlapped finalize batch=8 events=7 D=1152")
+    step = bench.LiteralStep(8, 1152, 7, seed=9)
+    step.step()
+    one = _snapshot(step)
+    step.step_overlap()
+    two = _snapshot(step)
+    for k in ("x_last", "z1", "gdz0", "gdz_last", "gbeta", "galpha"):
+        assert torch.equal(one[k], two[k]), k
