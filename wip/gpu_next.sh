@@ -10,5 +10,6 @@ step "focused tests" && timeout -k 10 900 python3 -u -m pytest -x -v --timeout 3
     tests/test_gpu_trib_empty_chunk.py tests/test_gpu_event.py > ../../gpurun_out/next_tests.log 2>&1 && \
 step "16-slot kernels" && timeout -k 10 600 python3 -u bench.py --mode kernels --slots 16 > ../../gpurun_out/next_k16.jsonl 2> ../../gpurun_out/next_k16.err && \
 step "two streams" && timeout -k 10 600 python3 -u bench.py --streams 2 --no-extra --no-cpu-baseline > ../../gpurun_out/next_s2.json 2> ../../gpurun_out/next_s2.err && \
-step "one stream" && timeout -k 10 600 python3 -u bench.py --streams 1 --no-extra --no-cpu-baseline > ../../gpurun_out/next_s1.json 2> ../../gpurun_out/next_s1.err
+step "one stream" && timeout -k 10 600 python3 -u bench.py --streams 1 --no-extra --no-cpu-baseline > ../../gpurun_out/next_s1.json 2> ../../gpurun_out/next_s1.err && \
+step "one stream, overlapped finalize" && timeout -k 10 600 python3 -u bench.py --overlap-finalize --no-extra --no-cpu-baseline > ../../gpurun_out/next_s1o.json 2> ../../gpurun_out/next_s1o.err
 rc=$?; tail -5 ../../gpurun_out/next_tests.log; exit $rc
