@@ -137,6 +137,9 @@
 #ifndef SIHC_K4_DOT2  // 1: 16-slot bf16 read / write / weight gradient sum bf16 pairs with v_dot2c_f32_bf16
 #define SIHC_K4_DOT2 1
 #endif
+#ifndef SIHC_RDW_MINE  // 4-slot bf16 reads with at least this many events: k_read_w (0: never)
+#define SIHC_RDW_MINE 8
+#endif
 #ifndef SIHC_RD2_U  // tokens per lane per iteration of the 16-slot dot2 read
 #define SIHC_RD2_U 4
 #endif
@@ -947,6 +950,91 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write_d2(const bf16_t* __
               store_vec<bf16_t, 2, NTS>(reinterpret_cast<bf16_t*>(ow + b0[u] + uy * row_w + ux * pix_w),
                                         acc[u][uy * K + ux]);
         }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// 4-slot bf16 read with many events, one output array per wave at a time:
+// out_e[m,c] = sum_s alpha[e,c,s] * x[m,s,c]. A block (4 waves) owns 128 channels (16
+// lanes x 8) and RDW_TT tokens. It stages its cell tile in LDS once, already as slot-pair
+// words (word (t, p, c) = x[t, 2p, c] | x[t, 2p + 1, c] << 16) and the weights' own pair
+// words alpha[e][c][2p..2p+1]; then wave w writes events w, w + 4, ... one at a time, each
+// as RDW_TT / 4 consecutive stores of 4 token rows x 256 bytes to that event's array
+// (k_read's lanes store all E arrays for every token pair: 24 arrays at once per wave).
+// The slot sum is two dot2 per channel.
+// ----------------------------------------------------------------------------------
+#ifndef RDW_TT  // tokens per block of k_read_w
+#define RDW_TT 32
+#endif
+template <int NTM>
+__global__ void __launch_bounds__(256) k_read_w(const bf16_t* __restrict__ x, const bf16_t* __restrict__ alpha,
+                                                PtrPack out, const int32_t* __restrict__ index, int E, Geo g,
+                                                int nslices) {
+  constexpr int K = 2, LX = 16, V = 8, BC = LX * V, RY = 4;
+  constexpr bool NTL = (NTM & 1) != 0, NTS = (NTM & 2) != 0;
+  extern __shared__ __align__(16) unsigned char smem_rw[];
+  uint32_t* xp = reinterpret_cast<uint32_t*>(smem_rw);  // [RDW_TT][2][BC] pair words
+  uint32_t* ap = xp + RDW_TT * 2 * BC;                   // [E][2][BC] pair words
+  const int blk = int(blockIdx.x), slice = blk % nslices, chunk = blk / nslices;
+  const int cs = slice * BC;
+  const int tid = int(threadIdx.x), wave = tid / 64, lane = tid % 64;
+  const int lx = lane % LX, ly = lane / LX;
+  const int m0 = chunk * RDW_TT;
+  const int tn = min(RDW_TT, g.M - m0);
+  // weights: word (e, p, c) = alpha[e][c][2p..2p+1] (zero past C)
+  const uint32_t* aw = reinterpret_cast<const uint32_t*>(alpha);
+  for (int i = tid; i < E * BC * 2; i += 256) {
+    const int e = i / (BC * 2), r = i - e * BC * 2, cl = r >> 1, pr = r & 1;
+    const int c = cs + cl;
+    ap[(e * 2 + pr) * BC + cl] = c < g.C ? aw[(int64_t(e) * g.C + c) * 2 + pr] : 0u;
+  }
+  // cell tile: unit u = (token t, channel group j): 4 slot vectors of 8 channels ->
+  // 8 pair words per slot pair
+  for (int u = tid; u < RDW_TT * LX; u += 256) {
+    const int t = u / LX, j = u % LX, c = cs + j * V;
+    if (t < tn && c < g.C) {
+      const int64_t p0 = cell_pixel0(m0 + t, g, index);
+      u32x4 v[4];
+#pragma unroll
+      for (int sl = 0; sl < 4; ++sl) v[sl] = ld<NTL>(reinterpret_cast<const u32x4*>(x + slot_offset<K>(p0, sl, g, c)));
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) {
+        const u32x4 a = v[2 * pr], b = v[2 * pr + 1];
+        u32x4 lo, hi;  // channels 0..3 and 4..7 of the group
+        lo[0] = pair_lo(a[0], b[0]);
+        lo[1] = pair_hi(a[0], b[0]);
+        lo[2] = pair_lo(a[1], b[1]);
+        lo[3] = pair_hi(a[1], b[1]);
+        hi[0] = pair_lo(a[2], b[2]);
+        hi[1] = pair_hi(a[2], b[2]);
+        hi[2] = pair_lo(a[3], b[3]);
+        hi[3] = pair_hi(a[3], b[3]);
+        u32x4* dst = reinterpret_cast<u32x4*>(xp + (t * 2 + pr) * BC + j * V);
+        dst[0] = lo;
+        dst[1] = hi;
+      }
+    }
+  }
+  __syncthreads();
+  const int c0 = cs + lx * V;
+  if (c0 >= g.C) return;  // no barrier below
+  for (int e = wave; e < E; e += 4) {
+    const u32x4* ae = reinterpret_cast<const u32x4*>(ap + e * 2 * BC + lx * V);
+    const u32x4 w00 = ae[0], w01 = ae[1];                       // pair 0, channels 0..3, 4..7
+    const u32x4 w10 = ae[BC / 4], w11 = ae[BC / 4 + 1];         // pair 1
+    bf16_t* dst = static_cast<bf16_t*>(const_cast<void*>(out.p[e]));
+#pragma unroll 2
+    for (int t = ly; t < tn; t += RY) {
+      const u32x4* xt = reinterpret_cast<const u32x4*>(xp + t * 2 * BC + lx * V);
+      const u32x4 x00 = xt[0], x01 = xt[1], x10 = xt[BC / 4], x11 = xt[BC / 4 + 1];
+      float acc[V];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc[k] = dot2(x10[k], w10[k], dot2(x00[k], w00[k], 0.f));
+        acc[4 + k] = dot2(x11[k], w11[k], dot2(x01[k], w01[k], 0.f));
+      }
+      store_vec<bf16_t, V, NTS>(dst + int64_t(m0 + t) * g.C + c0, acc);
     }
   }
 }
@@ -3116,6 +3204,21 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
   // 16 slots, bf16, 2-channel lanes, word-aligned weights: slot pairs summed by dot2 (the
   // weights' pair words staged in the same LDS bytes as the packed bf16 weights)
   const bool d2 = SIHC_K4_DOT2 && wb && cell == 4 && aligned(alpha, 4);
+  // 4 slots, bf16, 16-byte lanes, many events: one output array per wave at a time
+  if (SIHC_RDW_MINE > 0 && cell == 2 && dtype == SIHC_DTYPE_BF16 && V == 8 && events >= SIHC_RDW_MINE &&
+      aligned(alpha, 4)) {
+    const int slicesw = (channels + 127) / 128;
+    const int64_t chunksw = (int64_t(g.M) + RDW_TT - 1) / RDW_TT;
+    const size_t ldsw = size_t(RDW_TT + events) * 2 * 128 * sizeof(uint32_t);
+    const PtrPack pkw = pack(ptrs, events);
+    return with_hints<SIHC_RD_NTM>(read_hints(true, cell, events), [&](auto nt) {
+      constexpr int NT = decltype(nt)::value;
+      hipLaunchKernelGGL((k_read_w<NT>), dim3(blocks1d(slicesw, chunksw)), dim3(256), ldsw, st,
+                         static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(alpha), pkw, index, events, g,
+                         slicesw);
+      return check_launch(what);
+    });
+  }
   const Shape2D sh = cell == 2 ? shape_for(channels, V, SIHC_RW_BCG, events * S * wbytes)
                                : shape_for(channels, V, SIHC_RW_BCG_K4, events * S * wbytes, SIHC_RW_LDS_K4);
   const int tpb = sh.tl * rw_tokens_per_lane(cell, events, true);

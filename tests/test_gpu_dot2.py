@@ -74,3 +74,28 @@ def test_write_event_pairs(events, geom, add_x):
         assert_parity(got_cells, exp, BF16, what="write (gathered cells)")
     # a second call gives the same bits
     assert torch.equal(got, launch.write(x, ups, beta, add_x=add_x, index=idx))
+
+
+# 4-slot bf16 reads with 8+ events and 16-byte lanes (C % 8 == 0): the one-array-per-wave
+# kernel that stages the cell tile as slot-pair words (token tails: 5x5 and 7x7 grids;
+# channel tails: 136 = 128 + 8)
+GEOMS4 = [(3, 5, 136, False), (2, 7, 136, True), (1, 16, 1152, True)]
+
+
+@pytest.mark.parametrize("events", [8, 13, 24, 32])
+@pytest.mark.parametrize("geom", GEOMS4, ids=["b3-g5-c136", "b2-g7-c136-index", "b1-g16-c1152-index"])
+def test_read_4slot_wave_per_event(events, geom):
+    b, g, c, with_index = geom
+    announce(f"4-slot wave read b={b} g={g} c={c} events={events} index={with_index}")
+    torch.manual_seed(17 * events + c)
+    x = torch.randn(b, 2 * g, 2 * g, c, device="cuda").to(BF16)
+    alpha = (0.25 + 0.02 * torch.randn(events, c, 4, device="cuda")).to(BF16)
+    index = None
+    if with_index:
+        gen = torch.Generator().manual_seed(events + c)
+        index = torch.stack([torch.randperm(g * g, generator=gen) for _ in range(b)]).to(torch.int32)
+    got = launch.read(x, alpha, index=None if index is None else index.cuda())
+    xs = x.cpu() if index is None else O.cells_to_high(O.gather_cells(x.cpu(), index, 4))
+    exp = O.read(xs, alpha.cpu())
+    for e in range(events):
+        assert_parity(got[e], exp[e], BF16, what=f"read event {e}")

@@ -567,3 +567,69 @@ def run_fwd16(B, G, C, index=False, seed=0):
     e1 = ulps_ok(xo.view(np.uint16), rx); e2 = ulps_ok(zo, rz.reshape(-1))
     assert e1 <= 1.0 and e2 <= 1.0, (e1, e2)
     print(f"event_fwd16 B={B} G={G} C={C} index={index}: bounds ok, x_out {e1:.2f} ulp, z_out {e2:.2f} ulp", flush=True)
+
+def emu_read_w(xbits, abits, E, g, index, TT=32):
+    K, S, C, M = 2, 4, g.C, g.M
+    LX, V, BC, RY = 16, 8, 128, 4
+    slices = -(-C // BC); chunks = -(-M // TT); n = slices * chunks
+    X4 = xbits.view(np.uint32).reshape(-1, 4)
+    aw = Arr(len(abits) // 2, "alpha", data=abits.view(np.uint32))
+    outs = [Arr(M * C, f"out{e}", dtype=np.uint16) for e in range(E)]
+    written = [np.zeros(M * C, bool) for _ in range(E)]
+    for blk in range(n):
+        sl_ = blk % slices; chunk = blk // slices; cs = sl_ * BC
+        m0 = chunk * TT; tn = min(TT, M - m0)
+        lds = Arr((TT + E) * 2 * BC, "lds"); xp0 = 0; ap0 = TT * 2 * BC
+        for i in range(E * BC * 2):
+            e = i // (BC * 2); r = i - e * BC * 2; cl, pr = r >> 1, r & 1; c = cs + cl
+            lds[ap0 + (e * 2 + pr) * BC + cl] = aw[(e * C + c) * 2 + pr] if c < C else 0
+        for u in range(TT * LX):
+            t, j = u // LX, u % LX; c = cs + j * V
+            if t < tn and c < C:
+                p0 = cell_pixel0(m0 + t, g, index)
+                v = []
+                for s_ in range(4):
+                    off = (p0 + (s_ // K) * g.GK + (s_ % K)) * C + c
+                    assert off % 8 == 0
+                    if not (0 <= off // 8 < len(X4)): raise IndexError("x vector")
+                    v.append([int(q) for q in X4[off // 8]])
+                for pr in range(2):
+                    a, b = v[2 * pr], v[2 * pr + 1]
+                    words = [pair_lo(a[0], b[0]), pair_hi(a[0], b[0]), pair_lo(a[1], b[1]), pair_hi(a[1], b[1]),
+                             pair_lo(a[2], b[2]), pair_hi(a[2], b[2]), pair_lo(a[3], b[3]), pair_hi(a[3], b[3])]
+                    base = xp0 + (t * 2 + pr) * BC + j * V
+                    for k in range(8): lds[base + k] = words[k]
+        for tid in range(256):
+            wave, lane = tid // 64, tid % 64; lx, ly = lane % LX, lane // LX
+            c0 = cs + lx * V
+            if c0 >= C: continue
+            for e in range(wave, E, 4):
+                ae = ap0 + e * 2 * BC + lx * V
+                w0 = [lds[ae + k] for k in range(8)]; w1 = [lds[ae + BC + k] for k in range(8)]
+                for t in range(ly, tn, RY):
+                    xt = xp0 + t * 2 * BC + lx * V
+                    x0 = [lds[xt + k] for k in range(8)]; x1 = [lds[xt + BC + k] for k in range(8)]
+                    acc = [dot2(x1[k], w1[k], dot2(x0[k], w0[k], np.float32(0))) for k in range(8)]
+                    bits = bf16_bits(np.array(acc, np.float32))
+                    o = (m0 + t) * C + c0
+                    for k in range(8): outs[e][o + k] = bits[k]; written[e][o + k] = True
+    return [o.a for o in outs], written
+
+def run_read_w(B, G, C, E, index=False, seed=0):
+    rng = np.random.default_rng(seed)
+    g = Geo(B, G, 2, C)
+    idx = np.array([(m % g.GG * 7 + 3) % g.GG for m in range(g.M)], np.int32) if index else None
+    xbits = bf16_bits(rng.standard_normal(B * g.GK * g.GK * C))
+    abits = bf16_bits(0.25 + 0.02 * rng.standard_normal(E * C * 4))
+    outs, written = emu_read_w(xbits, abits, E, g, idx)
+    x = bf(xbits).astype(np.float64); a = bf(abits).astype(np.float64).reshape(E, C, 4)
+    worst = 0
+    for m in range(g.M):
+        p0 = cell_pixel0(m, g, idx)
+        xs = np.stack([x[slot_offset(p0, s, g, 0, K=2):slot_offset(p0, s, g, 0, K=2) + C] for s in range(4)])
+        ref = np.einsum('ecs,sc->ec', a, xs)
+        for e in range(E):
+            worst = max(worst, ulps_ok(outs[e][m * C:(m + 1) * C], ref[e]))
+    assert all(w.all() for w in written), "unwritten outputs"
+    assert worst <= 1.0, worst
+    print(f"read_w B={B} G={G} C={C} E={E} index={index}: bounds ok, all written, worst {worst:.3f} ulp", flush=True)
