@@ -57,6 +57,18 @@
 #ifndef SIHC_EV_UNROLL  // tokens per lane per loop iteration, per-event kernels
 #define SIHC_EV_UNROLL 2
 #endif
+#ifndef SIHC_EV_FWD16  // 1: 16-slot bf16 per-event forward on the register-lean kernel
+#define SIHC_EV_FWD16 1
+#endif
+#ifndef SIHC_EV_BWD16  // 1: 16-slot bf16 per-event backward on the register-lean kernel
+#define SIHC_EV_BWD16 1
+#endif
+#ifndef SIHC_EV16_MINW  // occupancy hint (min waves per SIMD) of the 16-slot per-event backward
+#define SIHC_EV16_MINW 2
+#endif
+#ifndef SIHC_EV_FWD_THREADS  // threads per one-shot block of the per-event forward (256 or 512)
+#define SIHC_EV_FWD_THREADS 256
+#endif
 #ifndef SIHC_EV_MINW  // occupancy hint (min waves per SIMD) of the per-event kernels
 #define SIHC_EV_MINW 1
 #endif
@@ -121,6 +133,18 @@
 #endif
 #ifndef SIHC_K4_BF16W  // 1: 16-slot read / write stage bf16 weights packed as bf16 in LDS
 #define SIHC_K4_BF16W 1
+#endif
+#ifndef SIHC_K4_DOT2  // 1: 16-slot bf16 read / write / weight gradient sum bf16 pairs with v_dot2c_f32_bf16
+#define SIHC_K4_DOT2 1
+#endif
+#ifndef SIHC_RDW_MINE  // 4-slot bf16 reads with at least this many events: k_read_w (0: never)
+#define SIHC_RDW_MINE 8
+#endif
+#ifndef SIHC_RD2_U  // tokens per lane per iteration of the 16-slot dot2 read
+#define SIHC_RD2_U 4
+#endif
+#ifndef SIHC_WR2_U  // tokens per lane per iteration of the 16-slot dot2 write
+#define SIHC_WR2_U 2
 #endif
 #ifndef SIHC_K2_BF16W  // the same for 4-slot read / write (8-channel lanes)
 #define SIHC_K2_BF16W 1
@@ -565,6 +589,128 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read(const T* __restrict_
 }
 
 // ----------------------------------------------------------------------------------
+// bf16 pair arithmetic (16-slot cells). A 32-bit word holds two bf16 values; pair_lo /
+// pair_hi gather the low / high halves of two words into one word (v_perm_b32), and
+// dot2 adds both products of two such words to an fp32 accumulator (v_dot2c_f32_bf16:
+// the bf16 products are exact in fp32), so one VALU instruction does two multiply-adds.
+// ----------------------------------------------------------------------------------
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pair_lo(uint32_t a, uint32_t b) {  // a.lo | b.lo << 16
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pair_hi(uint32_t a, uint32_t b) {  // a.hi | b.hi << 16
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), acc,
+                                         false);
+}
+
+// Stage the read weights of a 2-channel-lane slice [cs, cs + 2*BCG) for the dot2 read:
+// alpha [E][C][16] bf16 holds, for each (e, c), the 8 slot-pair words (slots 2p, 2p+1)
+// the read multiplies against. LDS layout [e][q][lane][4]: words (pair 2q, channel 0),
+// (2q, 1), (2q + 1, 0), (2q + 1, 1), so a lane reads an event's 16 words with four
+// consecutive-address 16-byte reads. Channels past C get zero words.
+__device__ __forceinline__ void stage_read_pairs(uint32_t* lds, const bf16_t* __restrict__ alpha, int E, int BCG,
+                                                 int cs, int C) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(alpha);
+  const int BC = 2 * BCG;
+  const int tid = threadIdx.y * blockDim.x + threadIdx.x;
+  const int nthr = blockDim.x * blockDim.y;
+  for (int i = tid; i < E * BC * 8; i += nthr) {  // global [e][c][pair]: coalesced
+    const int e = i / (BC * 8);
+    const int r = i - e * BC * 8;
+    const int cl = r >> 3, pr = r & 7;
+    const int c = cs + cl;
+    lds[((e * 4 + (pr >> 1)) * BCG + (cl >> 1)) * 4 + (pr & 1) * 2 + (cl & 1)] =
+        c < C ? w[(int64_t(e) * C + c) * 8 + pr] : 0u;
+  }
+  __syncthreads();
+}
+
+// ----------------------------------------------------------------------------------
+// 16-slot read in bf16: out_e[m,c] = sum_s alpha[e,c,s] * x[m,s,c] with the slot sum done
+// in pairs by dot2. A lane owns 2 channels (one word per token and slot) and U tokens;
+// each token's 16 slot words become 8 pair words per channel (pair_lo / pair_hi), which
+// then serve all E events. Per event and token a lane issues 16 dot2 (the fp32 kernel:
+// 32 FMAs plus the bf16 -> fp32 unpacking of its weights), and each 16-byte LDS weight
+// read feeds U tokens. Same block shape, token runs and hints as k_read.
+// ----------------------------------------------------------------------------------
+template <int U, int BCGT, int NTM>
+__global__ void __launch_bounds__(256, SIHC_RW_MINW) k_read_d2(const bf16_t* __restrict__ x,
+                                                 const bf16_t* __restrict__ alpha, PtrPack out,
+                                                 const int32_t* __restrict__ index, int E, Geo g, int gs,
+                                                 int nchunks, int nslices) {
+  constexpr int K = 4, S = 16;
+  constexpr bool NTL = (NTM & 1) != 0, NTS = (NTM & 2) != 0;  // hints: loads, stores
+  extern __shared__ float lds[];
+  const int BCG = BCGT ? BCGT : int(blockDim.x), TL = blockDim.y;
+  const int blk = logical_block<true>(), slice = blk % nslices, chunk = blk / nslices;
+  const int cs = slice * BCG * 2;
+  stage_read_pairs(reinterpret_cast<uint32_t*>(lds), alpha, E, BCG, cs, g.C);
+  const u32x4* wl = reinterpret_cast<const u32x4*>(lds);
+  const int c0 = cs + threadIdx.x * 2;
+  if (c0 >= g.C) return;
+  // slot s of a cell: carrier row s / 4, pixel s % 4 of the cell's 4-pixel run; in words
+  // (2 channels each, C even on this path) a pixel is C / 2 words and a row GK * C / 2
+  const int64_t row_w = int64_t(g.GK) * (g.C >> 1);
+  const int pix_w = g.C >> 1;
+  for (int64_t m0 = int64_t(chunk) * gs; m0 < g.M; m0 += int64_t(nchunks) * gs) {
+    const int64_t m_end = min(m0 + gs, int64_t(g.M));
+    for (int64_t mi = m0; mi < m_end; mi += U * TL) {
+      const int64_t m = mi + threadIdx.y;
+      bool ok[U];
+      int64_t zoff[U];
+      uint32_t xw[U][S];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        ok[u] = m + u * TL < m_end;
+        const int mu = int(ok[u] ? m + u * TL : mi);  // tail: reload a valid token, store nothing
+        const uint32_t* px = reinterpret_cast<const uint32_t*>(x + cell_pixel0(mu, g, index) * g.C + c0);
+        zoff[u] = int64_t(mu) * g.C + c0;
+#pragma unroll
+        for (int uy = 0; uy < K; ++uy)
+#pragma unroll
+          for (int ux = 0; ux < K; ++ux) xw[u][uy * K + ux] = ld<NTL>(px + uy * row_w + ux * pix_w);
+      }
+      load_fence();
+      uint32_t xp[U][S / 2][2];  // [token][slot pair][channel]
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int pr = 0; pr < S / 2; ++pr) {
+          xp[u][pr][0] = pair_lo(xw[u][2 * pr], xw[u][2 * pr + 1]);
+          xp[u][pr][1] = pair_hi(xw[u][2 * pr], xw[u][2 * pr + 1]);
+        }
+      for (int e = 0; e < E; ++e) {
+        float acc[U][2];
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc[u][0] = acc[u][1] = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const u32x4 w = wl[(e * 4 + q) * BCG + threadIdx.x];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            acc[u][0] = dot2(xp[u][2 * q][0], w[0], acc[u][0]);
+            acc[u][1] = dot2(xp[u][2 * q][1], w[1], acc[u][1]);
+            acc[u][0] = dot2(xp[u][2 * q + 1][0], w[2], acc[u][0]);
+            acc[u][1] = dot2(xp[u][2 * q + 1][1], w[3], acc[u][1]);
+          }
+        }
+        // all U chains are computed before the tail test (otherwise the compiler moves each
+        // token's chain into its store's branch, leaving two dependent chains at a time)
+#pragma unroll
+        for (int u = 0; u < U; ++u) asm volatile("" : "+v"(acc[u][0]), "+v"(acc[u][1]));
+        bf16_t* dst = static_cast<bf16_t*>(const_cast<void*>(out.p[e]));
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (ok[u]) store_vec<bf16_t, 2, NTS>(dst + zoff[u], acc[u]);
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------
 // write: out[m,s,c] = (add_x ? x : 0) + sum_e beta[e,c,s] * upd_e[m,c]
 // Events are consumed in groups of 4 (E padded to a multiple of 4 with zero weights
 // and a repeated valid pointer), so each group's 4 update loads issue together.
@@ -673,6 +819,223 @@ __global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write(const TX* __restric
         for (int s = 0; s < S; ++s) store_vec<TX, V, NTS>(out + slot_offset<K>(p0[u], s, g, c0), acc[u][s]);
       }
   }
+  }
+}
+
+// Stage the write weights of a 2-channel-lane slice for the dot2 write: word (j, s, c) =
+// beta[2j][c][s] | beta[2j + 1][c][s] << 16, the event pair j's weights of slot s (a zero
+// high half past the last event). LDS layout [j][s / 2][lane][4]: words (s even, channel
+// 0), (s even, 1), (s odd, 0), (s odd, 1), so a lane reads a pair's 32 words with eight
+// consecutive-address 16-byte reads.
+__device__ __forceinline__ void stage_write_pairs(uint32_t* lds, const bf16_t* __restrict__ beta, int E, int BCG,
+                                                  int cs, int C) {
+  const uint16_t* w = reinterpret_cast<const uint16_t*>(beta);
+  const int BC = 2 * BCG, J = (E + 1) / 2;
+  const int tid = threadIdx.y * blockDim.x + threadIdx.x;
+  const int nthr = blockDim.x * blockDim.y;
+  for (int i = tid; i < J * BC * 16; i += nthr) {  // [j][c][s]: consecutive slots of one (e, c)
+    const int j = i / (BC * 16);
+    const int r = i - j * BC * 16;
+    const int cl = r >> 4, sl = r & 15;
+    const int c = cs + cl;
+    uint32_t lo = 0u, hi = 0u;
+    if (c < C) {
+      lo = w[(int64_t(2 * j) * C + c) * 16 + sl];
+      if (2 * j + 1 < E) hi = w[(int64_t(2 * j + 1) * C + c) * 16 + sl];
+    }
+    lds[((j * 8 + (sl >> 1)) * BCG + (cl >> 1)) * 4 + (sl & 1) * 2 + (cl & 1)] = lo | (hi << 16);
+  }
+  __syncthreads();
+}
+
+// ----------------------------------------------------------------------------------
+// 16-slot write in bf16: out[m,s,c] = (add_x ? x[m,s,c] : 0) + sum_e beta[e,c,s] *
+// upd_e[m,c], the event sum done in pairs by dot2. A lane owns 2 channels and U tokens
+// (16 x 2 fp32 accumulators per token, started from the carrier when add_x); each event
+// pair's two update words per token become one pair word per channel (pair_lo /
+// pair_hi), multiplied against the staged weight pair of every slot: 32 dot2 per token
+// and pair (the fp32 kernel: 64 FMAs plus weight unpacking). The next pair's update
+// words are loaded before the current pair is summed. Same block shape, token runs and
+// hints as k_write.
+// ----------------------------------------------------------------------------------
+template <int U, bool ADD_X, int BCGT, int NTM>
+__global__ void __launch_bounds__(256, SIHC_RW_MINW) k_write_d2(const bf16_t* __restrict__ x, PtrPack upd,
+                                                  const bf16_t* __restrict__ beta, bf16_t* __restrict__ out,
+                                                  const int32_t* __restrict__ index, int E, Geo g, int gs,
+                                                  int nchunks, int nslices) {
+  constexpr int K = 4, S = 16;
+  constexpr bool NTL = (NTM & 1) != 0, NTS = (NTM & 2) != 0;  // hints: loads, stores
+  extern __shared__ float lds[];
+  const int BCG = BCGT ? BCGT : int(blockDim.x), TL = blockDim.y;
+  const int blk = logical_block<true>(), slice = blk % nslices, chunk = blk / nslices;
+  const int cs = slice * BCG * 2;
+  stage_write_pairs(reinterpret_cast<uint32_t*>(lds), beta, E, BCG, cs, g.C);
+  const u32x4* wl = reinterpret_cast<const u32x4*>(lds);
+  const int c0 = cs + threadIdx.x * 2;
+  if (c0 >= g.C) return;
+  const int J = (E + 1) / 2;
+  // carrier words (2 channels each, C even on this path): a pixel is C / 2 words, a
+  // carrier row GK * C / 2
+  const int64_t row_w = int64_t(g.GK) * (g.C >> 1);
+  const int pix_w = g.C >> 1;
+  const uint32_t* xw = reinterpret_cast<const uint32_t*>(x);
+  uint32_t* ow = reinterpret_cast<uint32_t*>(out);
+  for (int64_t m0 = int64_t(chunk) * gs; m0 < g.M; m0 += int64_t(nchunks) * gs) {
+    const int64_t m_end = min(m0 + gs, int64_t(g.M));
+    for (int64_t mi = m0; mi < m_end; mi += U * TL) {
+      const int64_t m = mi + threadIdx.y;
+      bool ok[U];
+      int64_t zoff[U], b0[U];
+      float acc[U][S][2];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        ok[u] = m + u * TL < m_end;
+        const int mu = int(ok[u] ? m + u * TL : mi);  // tail: reload a valid token, store nothing
+        b0[u] = (cell_pixel0(mu, g, index) * g.C + c0) >> 1;
+        zoff[u] = int64_t(mu) * g.C + c0;
+        if constexpr (ADD_X) {
+#pragma unroll
+          for (int uy = 0; uy < K; ++uy)
+#pragma unroll
+            for (int ux = 0; ux < K; ++ux) {
+              const uint32_t v = ld<NTL>(xw + b0[u] + uy * row_w + ux * pix_w);
+              acc[u][uy * K + ux][0] = __uint_as_float(v << 16);
+              acc[u][uy * K + ux][1] = __uint_as_float(v & 0xffff0000u);
+            }
+        } else {
+#pragma unroll
+          for (int s = 0; s < S; ++s) acc[u][s][0] = acc[u][s][1] = 0.f;
+        }
+      }
+      uint32_t zr[2][U];  // update words of the next event pair: [event of the pair][token]
+      auto issue = [&](int j) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const bf16_t* z = static_cast<const bf16_t*>(upd.p[min(2 * j + q, E - 1)]);
+#pragma unroll
+          for (int u = 0; u < U; ++u) zr[q][u] = ld<NTL>(reinterpret_cast<const uint32_t*>(z + zoff[u]));
+        }
+      };
+      issue(0);
+      for (int j = 0; j < J; ++j) {
+        uint32_t d[U][2];  // [token][channel]: (event 2j, event 2j + 1) pair words
+        const bool second = 2 * j + 1 < E;  // past the last event the pair's high half is zero
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const uint32_t w1 = second ? zr[1][u] : 0u;
+          d[u][0] = pair_lo(zr[0][u], w1);
+          d[u][1] = pair_hi(zr[0][u], w1);
+        }
+        if (j + 1 < J) issue(j + 1);
+        load_fence();
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const u32x4 w = wl[(j * 8 + q) * BCG + threadIdx.x];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            acc[u][2 * q][0] = dot2(d[u][0], w[0], acc[u][2 * q][0]);
+            acc[u][2 * q][1] = dot2(d[u][1], w[1], acc[u][2 * q][1]);
+            acc[u][2 * q + 1][0] = dot2(d[u][0], w[2], acc[u][2 * q + 1][0]);
+            acc[u][2 * q + 1][1] = dot2(d[u][1], w[3], acc[u][2 * q + 1][1]);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (ok[u]) {
+#pragma unroll
+          for (int uy = 0; uy < K; ++uy)
+#pragma unroll
+            for (int ux = 0; ux < K; ++ux)
+              store_vec<bf16_t, 2, NTS>(reinterpret_cast<bf16_t*>(ow + b0[u] + uy * row_w + ux * pix_w),
+                                        acc[u][uy * K + ux]);
+        }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// 4-slot bf16 read with many events, one output array per wave at a time:
+// out_e[m,c] = sum_s alpha[e,c,s] * x[m,s,c]. A block (4 waves) owns 128 channels (16
+// lanes x 8) and RDW_TT tokens. It stages its cell tile in LDS once, already as slot-pair
+// words (word (t, p, c) = x[t, 2p, c] | x[t, 2p + 1, c] << 16) and the weights' own pair
+// words alpha[e][c][2p..2p+1]; then wave w writes events w, w + 4, ... one at a time, each
+// as RDW_TT / 4 consecutive stores of 4 token rows x 256 bytes to that event's array
+// (k_read's lanes store all E arrays for every token pair: 24 arrays at once per wave).
+// The slot sum is two dot2 per channel.
+// ----------------------------------------------------------------------------------
+#ifndef RDW_TT  // tokens per block of k_read_w
+#define RDW_TT 32
+#endif
+template <int NTM>
+__global__ void __launch_bounds__(256) k_read_w(const bf16_t* __restrict__ x, const bf16_t* __restrict__ alpha,
+                                                PtrPack out, const int32_t* __restrict__ index, int E, Geo g,
+                                                int nslices) {
+  constexpr int K = 2, LX = 16, V = 8, BC = LX * V, RY = 4;
+  constexpr bool NTL = (NTM & 1) != 0, NTS = (NTM & 2) != 0;
+  extern __shared__ __align__(16) unsigned char smem_rw[];
+  uint32_t* xp = reinterpret_cast<uint32_t*>(smem_rw);  // [RDW_TT][2][BC] pair words
+  uint32_t* ap = xp + RDW_TT * 2 * BC;                   // [E][2][BC] pair words
+  const int blk = int(blockIdx.x), slice = blk % nslices, chunk = blk / nslices;
+  const int cs = slice * BC;
+  const int tid = int(threadIdx.x), wave = tid / 64, lane = tid % 64;
+  const int lx = lane % LX, ly = lane / LX;
+  const int m0 = chunk * RDW_TT;
+  const int tn = min(RDW_TT, g.M - m0);
+  // weights: word (e, p, c) = alpha[e][c][2p..2p+1] (zero past C)
+  const uint32_t* aw = reinterpret_cast<const uint32_t*>(alpha);
+  for (int i = tid; i < E * BC * 2; i += 256) {
+    const int e = i / (BC * 2), r = i - e * BC * 2, cl = r >> 1, pr = r & 1;
+    const int c = cs + cl;
+    ap[(e * 2 + pr) * BC + cl] = c < g.C ? aw[(int64_t(e) * g.C + c) * 2 + pr] : 0u;
+  }
+  // cell tile: unit u = (token t, channel group j): 4 slot vectors of 8 channels ->
+  // 8 pair words per slot pair
+  for (int u = tid; u < RDW_TT * LX; u += 256) {
+    const int t = u / LX, j = u % LX, c = cs + j * V;
+    if (t < tn && c < g.C) {
+      const int64_t p0 = cell_pixel0(m0 + t, g, index);
+      u32x4 v[4];
+#pragma unroll
+      for (int sl = 0; sl < 4; ++sl) v[sl] = ld<NTL>(reinterpret_cast<const u32x4*>(x + slot_offset<K>(p0, sl, g, c)));
+#pragma unroll
+      for (int pr = 0; pr < 2; ++pr) {
+        const u32x4 a = v[2 * pr], b = v[2 * pr + 1];
+        u32x4 lo, hi;  // channels 0..3 and 4..7 of the group
+        lo[0] = pair_lo(a[0], b[0]);
+        lo[1] = pair_hi(a[0], b[0]);
+        lo[2] = pair_lo(a[1], b[1]);
+        lo[3] = pair_hi(a[1], b[1]);
+        hi[0] = pair_lo(a[2], b[2]);
+        hi[1] = pair_hi(a[2], b[2]);
+        hi[2] = pair_lo(a[3], b[3]);
+        hi[3] = pair_hi(a[3], b[3]);
+        u32x4* dst = reinterpret_cast<u32x4*>(xp + (t * 2 + pr) * BC + j * V);
+        dst[0] = lo;
+        dst[1] = hi;
+      }
+    }
+  }
+  __syncthreads();
+  const int c0 = cs + lx * V;
+  if (c0 >= g.C) return;  // no barrier below
+  for (int e = wave; e < E; e += 4) {
+    const u32x4* ae = reinterpret_cast<const u32x4*>(ap + e * 2 * BC + lx * V);
+    const u32x4 w00 = ae[0], w01 = ae[1];                       // pair 0, channels 0..3, 4..7
+    const u32x4 w10 = ae[BC / 4], w11 = ae[BC / 4 + 1];         // pair 1
+    bf16_t* dst = static_cast<bf16_t*>(const_cast<void*>(out.p[e]));
+#pragma unroll 2
+    for (int t = ly; t < tn; t += RY) {
+      const u32x4* xt = reinterpret_cast<const u32x4*>(xp + t * 2 * BC + lx * V);
+      const u32x4 x00 = xt[0], x01 = xt[1], x10 = xt[BC / 4], x11 = xt[BC / 4 + 1];
+      float acc[V];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        acc[k] = dot2(x10[k], w10[k], dot2(x00[k], w00[k], 0.f));
+        acc[4 + k] = dot2(x11[k], w11[k], dot2(x01[k], w01[k], 0.f));
+      }
+      store_vec<bf16_t, V, NTS>(dst + int64_t(m0 + t) * g.C + c0, acc);
+    }
   }
 }
 
@@ -1327,59 +1690,220 @@ __global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgradz(const bf16_t* __
 }
 
 // ----------------------------------------------------------------------------------
+// 16-slot bf16 weight gradient with dot2 over token pairs: dW[e,s,c] partials =
+// sum_m z_e[m,c] * x[m,s,c], two tokens per instruction. The block, its event waves and
+// the double-buffered staging follow k_wgradz, but the LDS tiles interleave token pairs:
+// xt2[((tp * 16 + s) * 64 + cl)] holds x[t0 + 2tp, s, cs + cl] | x[t0 + 2tp + 1, s, cs + cl]
+// << 16, zt2[(tp * E + e) * 64 + cl] the same for z_e (a zero high half for the odd last
+// token of a tile). A thread stages both tokens of a pair (two 16-byte loads) and packs
+// them with pair_lo / pair_hi into two 16-byte LDS writes; a lane then reads one word per
+// (pair, slot) and per (pair, event) and issues 16 x EPL dot2 per token pair where
+// k_wgradz issues 32 x EPL FMAs plus the bf16 -> fp32 conversions of 2 x (16 + EPL)
+// 2-byte LDS reads. Partial rows as k_wgradz (the summation order differs: pairs).
+// NPQ: token-pair carrier vectors per thread; EPL: events per wave (lane).
+// ----------------------------------------------------------------------------------
+template <int NPQ, int EPL>
+__global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgradz_d2(const bf16_t* __restrict__ x, PtrPack z,
+                                                                   float* __restrict__ part,
+                                                                   const int32_t* __restrict__ index, int E, Geo g,
+                                                                   int tpb, int nslices) {
+  constexpr bool NTL = true;
+  constexpr int K = 4, S = 16, TT = SIHC_C16Z_TT, VS = 8, NV = C16_LANES / VS;
+  constexpr int TP = TT / 2;           // token pairs per tile
+  constexpr int NXP = TP * S * NV;     // carrier vector pairs per tile
+  constexpr int NZK = (EPL + 1) / 2;   // update events staged per lane (two lane halves)
+  static_assert(TT % 2 == 0 && TP * NV == C16_LANES / 2, "half a wave stages one event's token pairs");
+  using R = u32x4;
+  extern __shared__ __align__(16) unsigned char smem16[];
+  uint32_t* xt = reinterpret_cast<uint32_t*>(smem16);  // [TP][S][64] pair words
+  uint32_t* zt = xt + TP * S * C16_LANES;              // [TP][E][64] pair words
+  const int lane = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.y);
+  const int nw = blockDim.y, nthr = C16_LANES * nw, tid = wave * C16_LANES + lane;
+  const int e0 = wave * EPL;
+  const int blk = logical_block<false>(), slice = blk % nslices, chunk = blk / nslices;
+  const int cs = slice * C16_LANES, c = cs + lane;
+  const bool cok = c < g.C;
+  // this lane's update staging slot: lane half h (events k = h, h + 2, ... of the wave's
+  // share wave + k * nw), token pair zp, vector zj of the 64-channel row
+  const int zh = lane / (C16_LANES / 2), zp = (lane % (C16_LANES / 2)) / NV, zj = lane % NV;
+  const int zc = cs + zj * VS;
+  R xb[NPQ][2], zb[NZK][2];
+  // every load is issued at a clamped in-range address (commit drops what is not part of
+  // the tile), so no branch separates the loads
+  auto issue = [&](int t0, int tn) {
+    int64_t off[NPQ][2];
+#pragma unroll
+    for (int k = 0; k < NPQ; ++k) {
+      const int i = min(tid + k * nthr, NXP - 1);
+      const int row = i / NV, tp = row / S, cc = cs + (i % NV) * VS;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        off[k][h] = slot_offset<K>(cell_pixel0(t0 + min(2 * tp + h, tn - 1), g, index), row % S, g,
+                                   cc < g.C ? cc : cs);
+    }
+    int64_t zoff[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) zoff[h] = int64_t(t0 + min(2 * zp + h, tn - 1)) * g.C + (zc < g.C ? zc : cs);
+#pragma unroll
+    for (int k = 0; k < NPQ; ++k)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) xb[k][h] = ld<NTL>(reinterpret_cast<const R*>(x + off[k][h]));
+#pragma unroll
+    for (int k = 0; k < NZK; ++k) {
+      const int e = min(wave + (2 * k + zh) * nw, E - 1);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        zb[k][h] = ld<NTL>(reinterpret_cast<const R*>(static_cast<const bf16_t*>(z.p[e]) + zoff[h]));
+    }
+  };
+  // two 16-byte vectors of 8 channels (tokens 2tp, 2tp + 1) -> 8 pair words in channel order
+  auto put_pairs = [](uint32_t* dst, const R& a, const R& b, bool second) {
+    // word k of a vector holds channels 2k, 2k + 1: pair words 2k = pair_lo, 2k + 1 =
+    // pair_hi; words 0..1 of the vectors give channels 0..3 (lo), words 2..3 channels 4..7
+    R lo, hi;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t bl = second ? b[k] : 0u, bh = second ? b[k + 2] : 0u;
+      lo[2 * k] = pair_lo(a[k], bl);
+      lo[2 * k + 1] = pair_hi(a[k], bl);
+      hi[2 * k] = pair_lo(a[k + 2], bh);
+      hi[2 * k + 1] = pair_hi(a[k + 2], bh);
+    }
+    reinterpret_cast<R*>(dst)[0] = lo;
+    reinterpret_cast<R*>(dst)[1] = hi;
+  };
+  auto commit = [&](int tn) {
+#pragma unroll
+    for (int k = 0; k < NPQ; ++k) {
+      const int i = tid + k * nthr;
+      const int row = i / NV, tp = row / S, j = i % NV, cc = cs + j * VS;
+      if (i < NXP && 2 * tp < tn && cc < g.C) put_pairs(xt + row * C16_LANES + j * VS, xb[k][0], xb[k][1], 2 * tp + 1 < tn);
+    }
+#pragma unroll
+    for (int k = 0; k < NZK; ++k) {
+      const int e = wave + (2 * k + zh) * nw;
+      if (2 * k + zh < EPL && e < E && 2 * zp < tn && zc < g.C)
+        put_pairs(zt + (zp * E + e) * C16_LANES + zj * VS, zb[k][0], zb[k][1], 2 * zp + 1 < tn);
+    }
+  };
+  int zrow[EPL];  // this lane's event rows within a token pair's update rows (clamped)
+#pragma unroll
+  for (int q = 0; q < EPL; ++q) zrow[q] = min(e0 + q, E - 1);
+  float acc[EPL][S];
+#pragma unroll
+  for (int q = 0; q < EPL; ++q)
+#pragma unroll
+    for (int s = 0; s < S; ++s) acc[q][s] = 0.f;
+  const int m_begin = chunk * tpb;
+  const int m_end = min(m_begin + tpb, g.M);
+  if (m_begin < m_end) issue(m_begin, min(TT, m_end - m_begin));
+  for (int t0 = m_begin; t0 < m_end; t0 += TT) {
+    const int tn = min(TT, m_end - t0);
+    __syncthreads();  // the previous tile is fully reduced
+    commit(tn);
+    __syncthreads();
+    if (t0 + TT < m_end) issue(t0 + TT, min(TT, m_end - t0 - TT));
+    load_fence();
+    if (cok) {
+      for (int tp = 0; 2 * tp < tn; ++tp) {
+        uint32_t zv[EPL];
+#pragma unroll
+        for (int q = 0; q < EPL; ++q) zv[q] = zt[(tp * E + zrow[q]) * C16_LANES + lane];
+#pragma unroll
+        for (int sl = 0; sl < S; ++sl) {
+          const uint32_t xs = xt[(tp * S + sl) * C16_LANES + lane];
+#pragma unroll
+          for (int q = 0; q < EPL; ++q) acc[q][sl] = dot2(xs, zv[q], acc[q][sl]);
+        }
+      }
+    }
+  }
+  if (!cok) return;
+#pragma unroll
+  for (int q = 0; q < EPL; ++q) {
+    if (e0 + q < E) {
+      float* prow = part + (int64_t(chunk) * E + e0 + q) * S * g.C + c;
+#pragma unroll
+      for (int sl = 0; sl < S; ++sl) prow[int64_t(sl) * g.C] = acc[q][sl];
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------
 // Fixed-order sum of partial rows. part is [chunks][R][S][C]; row r of the result
 // goes to out0 + r*C*S ([R][C][S], `pair` == 0) or, with `pair`, row 0 -> out0 and
 // row 1 -> out1 (each [C][S]). Rows whose bit is set in zero_mask are written as
 // zeros without reading partials; a NULL destination row is skipped.
-// Block: 32 outputs x 8 chunk groups; each group sums its chunks in ascending order,
-// then the 8 group sums are added in ascending group order.
+// Block: 32 x NV outputs x 8 chunk groups; each group sums its chunks in ascending
+// order, then the 8 group sums are added in ascending group order. With NV = 4 a thread
+// reads four neighbouring outputs of each partial row as one 16-byte load (the group's
+// lanes then read 512 contiguous bytes per row instead of 128); the sums, and so the
+// bits, do not depend on NV.
 // ----------------------------------------------------------------------------------
-template <typename TO>
+template <typename TO, int NV>
 __device__ __forceinline__ void finalize_outputs(const float* __restrict__ part, TO* __restrict__ out0,
                                                  TO* __restrict__ out1, int chunks, int R, int S, int C, int pair,
                                                  int zero_mask, int block) {
   constexpr int FO = 32, FG = 8;
-  __shared__ float red[FG][FO];
-  const int64_t n = int64_t(R) * S * C;
+  __shared__ float red[FG][FO * NV];
+  const int64_t n = int64_t(R) * S * C, SC = int64_t(S) * C;  // NV > 1: SC % NV == 0
   const int o = threadIdx.x % FO, grp = threadIdx.x / FO;
-  const int64_t i = int64_t(block) * FO + o;
-  const int r = i < n ? int(i / (int64_t(S) * C)) : 0;
+  const int64_t i = (int64_t(block) * FO + o) * NV;  // this thread's first output
+  const bool live = i < n;
+  const int r = live ? int(i / SC) : 0;  // the NV outputs share the row r
   const bool zero = (zero_mask >> r) & 1;
-  float sum = 0.f;
-  if (i < n && !zero) {
+  float sum[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) sum[j] = 0.f;
+  if (live && !zero) {
     // 8 independent loads in flight per thread; the sum order stays ascending in k.
     int k = grp;
     for (; k + 7 * FG < chunks; k += 8 * FG) {
-      float v[8];
+      float v[8][NV];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] = part[int64_t(k + q * FG) * n + i];
+      for (int q = 0; q < 8; ++q) load_vec<float, NV>(part + int64_t(k + q * FG) * n + i, v[q]);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) sum += v[q];
+      for (int q = 0; q < 8; ++q)
+#pragma unroll
+        for (int j = 0; j < NV; ++j) sum[j] += v[q][j];
     }
-    for (; k < chunks; k += FG) sum += part[int64_t(k) * n + i];
-  }
-  red[grp][o] = sum;
-  __syncthreads();
-  if (grp != 0 || i >= n) return;
-  float t = 0.f;
+    for (; k < chunks; k += FG) {
+      float v[NV];
+      load_vec<float, NV>(part + int64_t(k) * n + i, v);
 #pragma unroll
-  for (int q = 0; q < FG; ++q) t += red[q][o];
-  const int rem = int(i - int64_t(r) * S * C);
-  const int s = rem / C;
-  const int c = rem - s * C;
+      for (int j = 0; j < NV; ++j) sum[j] += v[j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j) red[grp][o * NV + j] = sum[j];
+  __syncthreads();
+  if (grp != 0 || !live) return;
   TO* dst = pair ? (r == 0 ? out0 : out1) : (out0 ? out0 + int64_t(r) * C * S : nullptr);
-  if (dst) dst[int64_t(c) * S + s] = from_f32<TO>(zero ? 0.f : t);
+  if (!dst) return;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    float t = 0.f;
+#pragma unroll
+    for (int q = 0; q < FG; ++q) t += red[q][o * NV + j];
+    const int rem = int(i + j - int64_t(r) * SC);
+    const int s = rem / C;
+    const int c = rem - s * C;
+    dst[int64_t(c) * S + s] = from_f32<TO>(zero ? 0.f : t);
+  }
 }
 
-template <typename TO>
+template <typename TO, int NV>
 __global__ void __launch_bounds__(256) k_finalize(const float* __restrict__ part, TO* __restrict__ out0,
                                                   TO* __restrict__ out1, int chunks, int R, int S, int C,
                                                   int pair, int zero_mask) {
-  finalize_outputs<TO>(part, out0, out1, chunks, R, S, C, pair, zero_mask, int(blockIdx.x));
+  finalize_outputs<TO, NV>(part, out0, out1, chunks, R, S, C, pair, zero_mask, int(blockIdx.x));
 }
 
 // The per-event backward's finalize for up to SIHC_FINALIZE_BATCH deferred events in one
 // launch (grid.y = event): the same fixed-order sums as k_finalize, so the same bits.
+// Partial rows of the per-event backward are 16-byte aligned with 2 x S x C (S = 4 or 16)
+// entries, so every event takes the 4-wide path.
 #define SIHC_FINALIZE_BATCH 32
 struct FinalizeBatch {
   const float* part[SIHC_FINALIZE_BATCH];
@@ -1392,8 +1916,8 @@ struct FinalizeBatch {
 template <typename TO>
 __global__ void __launch_bounds__(256) k_finalize_batch(FinalizeBatch b, int S, int C) {
   const int e = int(blockIdx.y);
-  finalize_outputs<TO>(b.part[e], static_cast<TO*>(b.out0[e]), static_cast<TO*>(b.out1[e]), b.chunks[e], 2, S, C,
-                       1, b.zero_mask[e], int(blockIdx.x));
+  finalize_outputs<TO, 4>(b.part[e], static_cast<TO*>(b.out0[e]), static_cast<TO*>(b.out1[e]), b.chunks[e], 2, S, C,
+                          1, b.zero_mask[e], int(blockIdx.x));
 }
 
 template <typename TO>
@@ -1490,7 +2014,7 @@ __device__ __forceinline__ void load_weights(const T* __restrict__ w, int c0, fl
 }
 
 template <typename T, int V, int K, bool HAS_Z, bool NTL, bool NTS>
-__global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_fwd(const T* __restrict__ x, const T* __restrict__ dz,
+__global__ void __launch_bounds__(SIHC_EV_FWD_THREADS, SIHC_EV_MINW) k_event_fwd(const T* __restrict__ x, const T* __restrict__ dz,
                                                    const T* __restrict__ beta,
                                                    const T* __restrict__ alpha, T* __restrict__ xo,
                                                    T* __restrict__ zo, const int32_t* __restrict__ index,
@@ -1538,6 +2062,89 @@ __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_fwd(const T* __rest
 #pragma unroll
         for (int s = 0; s < S; ++s) store_vec<T, V, NTS>(xo + slot_offset<K>(p0[u], s, g, c0), xv[u][s]);
         if constexpr (HAS_Z) store_vec<T, V, NTS>(zo + zoff[u], zacc);
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// 16-slot bf16 per-event forward with 2-channel lanes: k_event_fwd's arithmetic (same
+// bits), with the carrier rows and the weights kept as bf16 words and each slot widened,
+// updated, rounded and stored in turn (k_event_fwd holds 2 x 16 x 2 fp32 carrier values
+// and 64 fp32 weights per lane at 16 slots: 145 VGPRs, 3 waves per SIMD).
+// ----------------------------------------------------------------------------------
+template <bool HAS_Z, bool NTL, bool NTS>
+__global__ void __launch_bounds__(SIHC_EV_FWD_THREADS, SIHC_EV_MINW) k_event_fwd16(const bf16_t* __restrict__ x,
+                                                     const bf16_t* __restrict__ dz,
+                                                     const bf16_t* __restrict__ beta,
+                                                     const bf16_t* __restrict__ alpha, bf16_t* __restrict__ xo,
+                                                     bf16_t* __restrict__ zo, const int32_t* __restrict__ index,
+                                                     Geo g, int tpb, int nslices) {
+  constexpr int K = 4, S = 16, V = 2;
+  constexpr int U = SIHC_EV_UNROLL;  // tokens per lane per iteration
+  const int BCG = blockDim.x, TL = blockDim.y;
+  const int blk = logical_block<true>(), slice = blk % nslices, chunk = blk / nslices;
+  const int c0 = (slice * BCG + threadIdx.x) * V;
+  if (c0 >= g.C) return;
+  uint32_t bw[16], aw[16];  // word v * 8 + p: channel c0 + v, slots 2p, 2p + 1
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const u32x4 r = reinterpret_cast<const u32x4*>(beta + int64_t(c0) * S)[q];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) bw[4 * q + k] = r[k];
+  }
+  if constexpr (HAS_Z) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x4 r = reinterpret_cast<const u32x4*>(alpha + int64_t(c0) * S)[q];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) aw[4 * q + k] = r[k];
+    }
+  }
+  auto wget = [](const uint32_t (&w)[16], int sl, int v) {
+    const uint32_t u = w[v * 8 + (sl >> 1)];
+    return __uint_as_float((sl & 1) ? (u & 0xffff0000u) : (u << 16));
+  };
+  const int64_t row_w = int64_t(g.GK) * (g.C >> 1);  // words per carrier row (C even here)
+  const int pix_w = g.C >> 1;
+  const uint32_t* xw = reinterpret_cast<const uint32_t*>(x);
+  uint32_t* xow = reinterpret_cast<uint32_t*>(xo);
+  const int m_begin = chunk * tpb;
+  const int m_end = min(m_begin + tpb, g.M);
+  for (int m = m_begin + threadIdx.y; m < m_end; m += U * TL) {
+    int64_t b0[U], zw[U];
+    bool ok[U];
+    uint32_t dr[U], xr[U][S];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      ok[u] = m + u * TL < m_end;
+      const int mu = ok[u] ? m + u * TL : m;  // tail: reload a valid token, store nothing
+      b0[u] = (cell_pixel0(mu, g, index) * g.C + c0) >> 1;
+      zw[u] = (int64_t(mu) * g.C + c0) >> 1;
+      dr[u] = ld<NTL>(reinterpret_cast<const uint32_t*>(dz) + zw[u]);
+#pragma unroll
+      for (int uy = 0; uy < K; ++uy)
+#pragma unroll
+        for (int ux = 0; ux < K; ++ux) xr[u][uy * K + ux] = ld<NTL>(xw + b0[u] + uy * row_w + ux * pix_w);
+    }
+    load_fence();
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float d[V] = {__uint_as_float(dr[u] << 16), __uint_as_float(dr[u] & 0xffff0000u)};
+      float zacc[V] = {0.f, 0.f};
+#pragma unroll
+      for (int sl = 0; sl < S; ++sl) {
+        float xv[V] = {__uint_as_float(xr[u][sl] << 16), __uint_as_float(xr[u][sl] & 0xffff0000u)};
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+          xv[v] = round_as<bf16_t>(fmaf(wget(bw, sl, v), d[v], xv[v]));
+          if constexpr (HAS_Z) zacc[v] = fmaf(wget(aw, sl, v), xv[v], zacc[v]);
+        }
+        if (ok[u])
+          store_vec<bf16_t, V, NTS>(reinterpret_cast<bf16_t*>(xow + b0[u] + (sl / K) * row_w + (sl % K) * pix_w), xv);
+      }
+      if constexpr (HAS_Z) {
+        if (ok[u]) store_vec<bf16_t, V, NTS>(zo + 2 * zw[u], zacc);
       }
     }
   }
@@ -1676,6 +2283,146 @@ __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_bwd(const T* __rest
       const int v = r - s * V;
       const int c = cs + lane * V + v;
       if (c < g.C) prow[(int64_t(w) * S + s) * g.C + c] = sum;
+    });
+  }
+}
+
+// ----------------------------------------------------------------------------------
+// 16-slot bf16 per-event backward with 2-channel lanes: k_event_bwd's arithmetic in the
+// same order (so the same bits), one token per lane per iteration, and the weights and
+// loaded rows kept as bf16 words, widened where they are used. A lane's 16-slot cell
+// otherwise holds 68 loaded values per token beside 64 accumulators and 64 weights:
+// k_event_bwd at 16 slots needs 334 VGPRs with two tokens per lane (one wave per SIMD).
+// A lane reads its channel pair's 16-slot weight rows ([C][16] bf16: 8 words per channel,
+// word p = slots 2p, 2p + 1) with four 16-byte loads. The token order per thread equals
+// k_event_bwd's (tokens ty, ty + TL, ... of each group), so the partial rows are the same.
+// ----------------------------------------------------------------------------------
+template <bool HAS_H, bool HAS_G, bool HAS_W, bool STORE_T, bool NTL, bool NTS>
+__global__ void __launch_bounds__(256, SIHC_EV16_MINW) k_event_bwd16(const bf16_t* __restrict__ gxo,
+                                                     const bf16_t* __restrict__ gzo,
+                                                     const bf16_t* __restrict__ xo, const bf16_t* __restrict__ dz,
+                                                     const bf16_t* __restrict__ beta,
+                                                     const bf16_t* __restrict__ alpha, bf16_t* __restrict__ gx,
+                                                     bf16_t* __restrict__ gdz, float* __restrict__ part,
+                                                     const int32_t* __restrict__ index, Geo g, int gs, int nchunks,
+                                                     int nslices) {
+  constexpr int K = 4, S = 16, V = 2;
+  extern __shared__ float red[];
+  const int BCG = blockDim.x, TL = blockDim.y;
+  const int BC = BCG * V;
+  const int blk = logical_block<true>(), slice = blk % nslices, chunk = blk / nslices;
+  const int c0 = slice * BC + threadIdx.x * V;
+  float db[S][V], da[S][V];
+#pragma unroll
+  for (int sl = 0; sl < S; ++sl)
+#pragma unroll
+    for (int v = 0; v < V; ++v) db[sl][v] = da[sl][v] = 0.f;
+  // word w of a weight row pair: channel w / 8, slots 2 (w % 8), 2 (w % 8) + 1
+  auto wget = [](const uint32_t (&w)[16], int sl, int v) {
+    const uint32_t u = w[v * 8 + (sl >> 1)];
+    return __uint_as_float((sl & 1) ? (u & 0xffff0000u) : (u << 16));
+  };
+  auto lo_f = [](uint32_t u) { return __uint_as_float(u << 16); };
+  auto hi_f = [](uint32_t u) { return __uint_as_float(u & 0xffff0000u); };
+  if (c0 < g.C) {
+    uint32_t bw[16], aw[16];
+    if constexpr (HAS_W) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x4 r = reinterpret_cast<const u32x4*>(beta + int64_t(c0) * S)[q];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) bw[4 * q + k] = r[k];
+      }
+    }
+    if constexpr (HAS_G) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x4 r = reinterpret_cast<const u32x4*>(alpha + int64_t(c0) * S)[q];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) aw[4 * q + k] = r[k];
+      }
+    }
+    const int64_t M = g.M;
+    const int64_t row_w = int64_t(g.GK) * (g.C >> 1);  // words per carrier row (C even here)
+    const int pix_w = g.C >> 1;
+    const uint32_t* gxw = reinterpret_cast<const uint32_t*>(gxo);
+    const uint32_t* xow = reinterpret_cast<const uint32_t*>(xo);
+    uint32_t* gxo_w = reinterpret_cast<uint32_t*>(gx);
+    for (int64_t m0 = int64_t(chunk) * gs; m0 < M; m0 += int64_t(nchunks) * gs) {
+      const int64_t m_end = min(m0 + gs, M);
+      for (int64_t mi = m0; mi < m_end; mi += TL) {
+        const int64_t mt = mi + threadIdx.y;
+        const bool ok = mt < m_end;
+        const int mu = int(ok ? mt : mi);  // tail: reload the iteration's first token
+        const int64_t b0 = (cell_pixel0(mu, g, index) * g.C + c0) >> 1;
+        const int64_t zw = (int64_t(mu) * g.C + c0) >> 1;
+        uint32_t gzr = 0u, dr = 0u, tr[S], xr[S];
+        if constexpr (HAS_G) gzr = ld<NTL>(reinterpret_cast<const uint32_t*>(gzo) + zw);
+        if constexpr (HAS_W) dr = ld<NTL>(reinterpret_cast<const uint32_t*>(dz) + zw);
+#pragma unroll
+        for (int uy = 0; uy < K; ++uy)
+#pragma unroll
+          for (int ux = 0; ux < K; ++ux) {
+            const int64_t o = b0 + uy * row_w + ux * pix_w;
+            tr[uy * K + ux] = HAS_H ? ld<NTL>(gxw + o) : 0u;
+            if constexpr (HAS_G) xr[uy * K + ux] = ld<NTL>(xow + o);
+          }
+        load_fence();
+        // a tail token adds exactly nothing: every loaded value is zeroed (a zero factor
+        // alone would turn an Inf in the repeated token into NaN), and nothing is stored
+        if (!ok) {
+          gzr = dr = 0u;
+#pragma unroll
+          for (int sl = 0; sl < S; ++sl) tr[sl] = xr[sl] = 0u;
+        }
+        const float gz[V] = {lo_f(gzr), hi_f(gzr)}, d[V] = {lo_f(dr), hi_f(dr)};
+        float gd[V] = {0.f, 0.f};
+#pragma unroll
+        for (int sl = 0; sl < S; ++sl) {
+          float t[V] = {lo_f(tr[sl]), hi_f(tr[sl])};
+#pragma unroll
+          for (int v = 0; v < V; ++v) {
+            if constexpr (HAS_G) {
+              const float xv = v ? hi_f(xr[sl]) : lo_f(xr[sl]);
+              da[sl][v] = fmaf(xv, gz[v], da[sl][v]);
+              t[v] = fmaf(wget(aw, sl, v), gz[v], t[v]);
+            }
+            if constexpr (HAS_W) {
+              gd[v] = fmaf(wget(bw, sl, v), t[v], gd[v]);
+              db[sl][v] = fmaf(d[v], t[v], db[sl][v]);
+            }
+          }
+          if constexpr (STORE_T) {
+            if (ok) {
+              const int uy = sl / K, ux = sl % K;
+              store_vec<bf16_t, V, NTS>(reinterpret_cast<bf16_t*>(gxo_w + b0 + uy * row_w + ux * pix_w), t);
+            }
+          }
+        }
+        if constexpr (HAS_W) {
+          if (ok) store_vec<bf16_t, V, NTS>(gdz + (int64_t(mu) * g.C + c0), gd);
+        }
+      }
+    }
+  }
+  // Block reduction of the [S][V] accumulators, as k_event_bwd: partial rows [2][S][C].
+  float* prow = part + int64_t(chunk) * 2 * S * g.C;
+  const int cs = slice * BC;
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    if ((w == 0 && !HAS_W) || (w == 1 && !HAS_G)) continue;
+    float flat[S * V];
+#pragma unroll
+    for (int sl = 0; sl < S; ++sl)
+#pragma unroll
+      for (int v = 0; v < V; ++v) flat[sl * V + v] = w == 0 ? db[sl][v] : da[sl][v];
+    block_reduce_rows<S * V>(flat, red, [&](int i, float sum) {
+      const int lane = i / (S * V);
+      const int r = i - lane * S * V;
+      const int sl = r / V;
+      const int v = r - sl * V;
+      const int c = cs + lane * V + v;
+      if (c < g.C) prow[(int64_t(w) * S + sl) * g.C + c] = sum;
     });
   }
 }
@@ -2110,13 +2857,24 @@ int fill_zero(int dtype, void* out, int64_t n, hipStream_t st, const char* what)
 int launch_finalize(const char* what, const float* part, void* out0, void* out1, int chunks, int R, int S, int C,
                     bool pair, int zero_mask, int out_dtype, hipStream_t st) {
   const int64_t n = int64_t(R) * S * C;
-  const unsigned blocks = unsigned((n + 31) / 32);
-  if (out_dtype == SIHC_DTYPE_F32) {
-    hipLaunchKernelGGL((k_finalize<float>), dim3(blocks), dim3(256), 0, st, part, static_cast<float*>(out0),
-                       static_cast<float*>(out1), chunks, R, S, C, pair ? 1 : 0, zero_mask);
+  // 4 outputs per thread when they never straddle a row and the rows are 16-byte aligned
+  const bool wide = (int64_t(S) * C) % 4 == 0 && aligned(part, 16);
+  auto go = [&](auto nv) {
+    constexpr int NV = decltype(nv)::value;
+    const unsigned blocks = unsigned((n + 32 * NV - 1) / (32 * NV));
+    if (out_dtype == SIHC_DTYPE_F32) {
+      hipLaunchKernelGGL((k_finalize<float, NV>), dim3(blocks), dim3(256), 0, st, part, static_cast<float*>(out0),
+                         static_cast<float*>(out1), chunks, R, S, C, pair ? 1 : 0, zero_mask);
+    } else {
+      hipLaunchKernelGGL((k_finalize<bf16_t, NV>), dim3(blocks), dim3(256), 0, st, part,
+                         static_cast<bf16_t*>(out0), static_cast<bf16_t*>(out1), chunks, R, S, C, pair ? 1 : 0,
+                         zero_mask);
+    }
+  };
+  if (wide) {
+    go(std::integral_constant<int, 4>{});
   } else {
-    hipLaunchKernelGGL((k_finalize<bf16_t>), dim3(blocks), dim3(256), 0, st, part, static_cast<bf16_t*>(out0),
-                       static_cast<bf16_t*>(out1), chunks, R, S, C, pair ? 1 : 0, zero_mask);
+    go(std::integral_constant<int, 1>{});
   }
   return check_launch(what);
 }
@@ -2259,12 +3017,26 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
             constexpr int NQ = decltype(nq)::value;
             constexpr int EP = decltype(ep)::value;
             const size_t ldsz = size_t(SIHC_C16Z_TT) * (KZ * KZ + events) * C16_LANES * sizeof(bf16_t);
+            // 16 slots: token pairs summed by dot2 (the same LDS bytes, NQ / 2 vector pairs
+            // per thread)
+            constexpr int NPQ = (NQ + 1) / 2;
+            constexpr bool D2 = SIHC_K4_DOT2 && KZ == 4;
+            const void* kfn;
+            if constexpr (D2) {
+              kfn = reinterpret_cast<const void*>(&k_wgradz_d2<NPQ, EP>);
+            } else {
+              kfn = reinterpret_cast<const void*>(&k_wgradz<KZ, NQ, EP>);
+            }
             // whole rounds of resident blocks, so the last round is not part-empty
-            const void* kfn = reinterpret_cast<const void*>(&k_wgradz<KZ, NQ, EP>);
             chunks = whole_rounds(slicesz, max_chunks, resident_blocks(kfn, C16_LANES * nw, ldsz));
             const int tpbz = int((int64_t(g.M) + chunks - 1) / chunks);
-            hipLaunchKernelGGL((k_wgradz<KZ, NQ, EP>), dim3(blocks1d(slicesz, chunks)), dim3(C16_LANES, nw), ldsz, st,
-                               reinterpret_cast<const bf16_t*>(x), pk, part, index, events, g, tpbz, slicesz);
+            if constexpr (D2) {
+              hipLaunchKernelGGL((k_wgradz_d2<NPQ, EP>), dim3(blocks1d(slicesz, chunks)), dim3(C16_LANES, nw), ldsz,
+                                 st, reinterpret_cast<const bf16_t*>(x), pk, part, index, events, g, tpbz, slicesz);
+            } else {
+              hipLaunchKernelGGL((k_wgradz<KZ, NQ, EP>), dim3(blocks1d(slicesz, chunks)), dim3(C16_LANES, nw), ldsz,
+                                 st, reinterpret_cast<const bf16_t*>(x), pk, part, index, events, g, tpbz, slicesz);
+            }
           };
           // events per lane: the first candidate giving 4 or 8 event waves (0: none)
           auto balanced_epl = [&](std::initializer_list<int> cands) {
@@ -2429,6 +3201,24 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
   const bool wb = dtype == SIHC_DTYPE_BF16 &&
                   ((SIHC_K4_BF16W && cell == 4 && V == 2) || (SIHC_K2_BF16W && cell == 2 && V == 8));
   const int wbytes = wb ? 2 : 4;
+  // 16 slots, bf16, 2-channel lanes, word-aligned weights: slot pairs summed by dot2 (the
+  // weights' pair words staged in the same LDS bytes as the packed bf16 weights)
+  const bool d2 = SIHC_K4_DOT2 && wb && cell == 4 && aligned(alpha, 4);
+  // 4 slots, bf16, 16-byte lanes, many events: one output array per wave at a time
+  if (SIHC_RDW_MINE > 0 && cell == 2 && dtype == SIHC_DTYPE_BF16 && V == 8 && events >= SIHC_RDW_MINE &&
+      aligned(alpha, 4)) {
+    const int slicesw = (channels + 127) / 128;
+    const int64_t chunksw = (int64_t(g.M) + RDW_TT - 1) / RDW_TT;
+    const size_t ldsw = size_t(RDW_TT + events) * 2 * 128 * sizeof(uint32_t);
+    const PtrPack pkw = pack(ptrs, events);
+    return with_hints<SIHC_RD_NTM>(read_hints(true, cell, events), [&](auto nt) {
+      constexpr int NT = decltype(nt)::value;
+      hipLaunchKernelGGL((k_read_w<NT>), dim3(blocks1d(slicesw, chunksw)), dim3(256), ldsw, st,
+                         static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(alpha), pkw, index, events, g,
+                         slicesw);
+      return check_launch(what);
+    });
+  }
   const Shape2D sh = cell == 2 ? shape_for(channels, V, SIHC_RW_BCG, events * S * wbytes)
                                : shape_for(channels, V, SIHC_RW_BCG_K4, events * S * wbytes, SIHC_RW_LDS_K4);
   const int tpb = sh.tl * rw_tokens_per_lane(cell, events, true);
@@ -2462,6 +3252,15 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
                                      static_cast<const T*>(alpha), pk, index, events, g, gs, int(chunks), sh.slices);
                   return check_launch(what);
                 };
+                if constexpr (KK == 4 && VV == 2 && std::is_same_v<T, bf16_t>) {
+                  if (d2) {
+                    hipLaunchKernelGGL((k_read_d2<SIHC_RD2_U, BB, NT>), dim3(blocks1d(sh.slices, chunks)),
+                                       dim3(sh.bcg, sh.tl), lds, st, static_cast<const T*>(x),
+                                       static_cast<const T*>(alpha), pk, index, events, g, gs, int(chunks),
+                                       sh.slices);
+                    return check_launch(what);
+                  }
+                }
                 if constexpr (((KK == 4 && VV == 2) || (KK == 2 && VV == 8)) && std::is_same_v<T, bf16_t>) {
                   if (wb) return go(std::true_type{});
                 }
@@ -2501,6 +3300,9 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
   const bool wb = w_dtype == SIHC_DTYPE_BF16 &&
                   ((SIHC_K4_BF16W && cell == 4 && V == 2) || (SIHC_K2_BF16W && cell == 2 && V == 8));
   const int wbytes = wb ? 2 : 4;
+  // 16 slots, bf16 carrier, updates and weights, 2-channel lanes: event pairs summed by
+  // dot2 (pair words staged in no more LDS than the packed bf16 weights)
+  const bool d2 = SIHC_K4_DOT2 && wb && cell == 4 && x_dtype == SIHC_DTYPE_BF16;
   const Shape2D sh = cell == 2 ? shape_for(channels, V, SIHC_RW_BCG, E4 * S * wbytes)
                                : shape_for(channels, V, SIHC_RW_BCG_K4, E4 * S * wbytes, SIHC_RW_LDS_K4);
   const int tpb = sh.tl * rw_tokens_per_lane(cell, E4);
@@ -2537,6 +3339,15 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
                                        int(chunks), sh.slices);
                     return check_launch(what);
                   };
+                  if constexpr (KK == 4 && VV == 2 && std::is_same_v<TX, bf16_t> && std::is_same_v<TW, bf16_t>) {
+                    if (d2) {
+                      hipLaunchKernelGGL((k_write_d2<SIHC_WR2_U, AX, BB, NT>), dim3(blocks1d(sh.slices, chunks)),
+                                         dim3(sh.bcg, sh.tl), lds, st, static_cast<const TX*>(x), pk,
+                                         static_cast<const TW*>(beta), static_cast<TX*>(out), index, events, g, gs,
+                                         int(chunks), sh.slices);
+                      return check_launch(what);
+                    }
+                  }
                   if constexpr (((KK == 4 && VV == 2) || (KK == 2 && VV == 8)) && std::is_same_v<TW, bf16_t>) {
                     if (wb) return go(std::true_type{});
                   }
@@ -2702,7 +3513,8 @@ int sihc_event_forward(const void* x, const void* dz, const void* beta, const vo
   while (V > 1 && (!aligned(beta, std::min(16, V * S * es)) ||
                    (alpha_next && !aligned(alpha_next, std::min(16, V * S * es)))))
     V /= 2;
-  const Shape2D sh = shape_for(channels, V, SIHC_EV_BCG, 0);
+  Shape2D sh = shape_for(channels, V, SIHC_EV_BCG, 0);
+  sh.tl = SIHC_EV_FWD_THREADS / sh.bcg;  // one-shot blocks of SIHC_EV_FWD_THREADS threads
   const int tpb = sh.tl * SIHC_EV_TPT;
   const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -2718,6 +3530,13 @@ int sihc_event_forward(const void* x, const void* dz, const void* beta, const vo
           return with_bool(alpha_next != nullptr, [&](auto hz) {
             constexpr bool HZ = decltype(hz)::value;
             constexpr bool NTL = (SIHC_EV_FWD_NT & 1) != 0, NTS = (SIHC_EV_FWD_NT & 2) != 0;
+            if constexpr (SIHC_EV_FWD16 && KK == 4 && VV == 2 && std::is_same_v<T, bf16_t>) {
+              hipLaunchKernelGGL((k_event_fwd16<HZ, NTL, NTS>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl),
+                                 0, st, static_cast<const T*>(x), static_cast<const T*>(dz),
+                                 static_cast<const T*>(beta), static_cast<const T*>(alpha_next),
+                                 static_cast<T*>(x_out), static_cast<T*>(z_out), index, g, tpb, sh.slices);
+              return check_launch(what);
+            }
             hipLaunchKernelGGL((k_event_fwd<T, VV, KK, HZ, NTL, NTS>), dim3(blocks1d(sh.slices, chunks)), dim3(sh.bcg, sh.tl), 0,
                                st, static_cast<const T*>(x), static_cast<const T*>(dz), static_cast<const T*>(beta),
                                static_cast<const T*>(alpha_next), static_cast<T*>(x_out), static_cast<T*>(z_out),
@@ -2803,12 +3622,28 @@ static int event_backward_impl(const char* what, const void* grad_x_out, const v
             auto go = [&](auto hg, auto hw, auto stt) {
               constexpr bool HG = decltype(hg)::value, HW = decltype(hw)::value, STT = decltype(stt)::value;
               constexpr bool NTL = (SIHC_EV_BWD_NT & 1) != 0, NTS = (SIHC_EV_BWD_NT & 2) != 0;
-              const void* kfn = reinterpret_cast<const void*>(&k_event_bwd<T, VV, KK, HH, HG, HW, STT, NTL, NTS>);
+              // 16-slot bf16 cells with 2-channel lanes: the register-lean kernel
+              constexpr bool B16 = SIHC_EV_BWD16 && KK == 4 && VV == 2 && std::is_same_v<T, bf16_t>;
+              const void* kfn;
+              if constexpr (B16) {
+                kfn = reinterpret_cast<const void*>(&k_event_bwd16<HH, HG, HW, STT, NTL, NTS>);
+              } else {
+                kfn = reinterpret_cast<const void*>(&k_event_bwd<T, VV, KK, HH, HG, HW, STT, NTL, NTS>);
+              }
               chunks = whole_rounds(sh.slices, max_chunks, resident_blocks(kfn, sh.bcg * sh.tl, lds));
               // token groups: a multiple of one loop iteration (SIHC_EV_UNROLL x TL tokens);
               // group 0 means one contiguous run of tokens per chunk
               const int gs = group_tokens(KK == 2 ? SIHC_EV_GROUP : SIHC_EV_GROUP_K4, g.M, chunks,
                                           SIHC_EV_UNROLL * sh.tl);
+              if constexpr (B16) {
+                hipLaunchKernelGGL((k_event_bwd16<HH, HG, HW, STT, NTL, NTS>), dim3(blocks1d(sh.slices, chunks)),
+                                   dim3(sh.bcg, sh.tl), lds, st, static_cast<const T*>(grad_x_out),
+                                   static_cast<const T*>(grad_z_out), static_cast<const T*>(x_out),
+                                   static_cast<const T*>(dz), static_cast<const T*>(beta),
+                                   static_cast<const T*>(alpha_next), static_cast<T*>(grad_x),
+                                   static_cast<T*>(grad_dz), part, index, g, gs, chunks, sh.slices);
+                return check_launch(what);
+              }
               hipLaunchKernelGGL((k_event_bwd<T, VV, KK, HH, HG, HW, STT, NTL, NTS>), dim3(blocks1d(sh.slices, chunks)),
                                  dim3(sh.bcg, sh.tl), lds, st, static_cast<const T*>(grad_x_out),
                                  static_cast<const T*>(grad_z_out), static_cast<const T*>(x_out),
@@ -2883,7 +3718,7 @@ int sihc_event_finalize(int n, const void* const* workspaces, const int* info, v
       return fail(SIHC_ERR_INVALID, "%s: null gradient of event %d", what, i);
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const unsigned bx = unsigned((int64_t(2) * S * channels + 31) / 32);
+  const unsigned bx = unsigned((int64_t(2) * S * channels + 127) / 128);  // 128 outputs per block
   for (int i0 = 0; i0 < n; i0 += SIHC_FINALIZE_BATCH) {
     FinalizeBatch b{};
     int nb = 0;
