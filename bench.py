@@ -48,10 +48,10 @@ def parse_args():
     p.add_argument("--channels", type=int, default=1152)
     p.add_argument("--events", type=int, default=56)
     p.add_argument("--seed", type=int, default=2)
-    p.add_argument("--streams", type=int, choices=(1, 2), default=1,
-                   help="config 2 as one chain, or two half-batch chains on two HIP streams")
-    p.add_argument("--overlap-finalize", action="store_true",
-                   help="one-stream step with half of the deferred finalize on a second stream")
+    p.add_argument("--finalize", choices=("chain", "deferred", "overlap"), default="chain",
+                   help="weight-gradient finalize of the backward: in the next launch's trailing blocks "
+                        "(sihc_event_backward_chain), one deferred launch per 32 events after the last event, "
+                        "or half of that deferred finalize on a second stream")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true", help="skip the secondary config 1/3/4 figures")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
@@ -120,14 +120,14 @@ class LiteralStep:
         self.galpha = torch.empty_like(self.alpha)
         self.gbeta = torch.empty_like(self.beta)
         nws = self.L.sihc_event_backward_workspace_size(B, G, K, C)
-        # one workspace per backward call: each keeps its partial rows until the one
-        # deferred finalize after the last event (E x 9.4 MB at the benchmark shape)
-        # (slot E: the first read's adjoint, whose rows must not overwrite event 0's)
+        # one workspace per backward call (sihc_event_backward_workspace_size: 1,024 chunks x
+        # 2 x 4 slots x 1152 channels x 4 B = 37.7 MB at the benchmark shape); under the
+        # deferred schedule each keeps its partial rows until the finalize after the last
+        # event (slot E: the first read's adjoint, whose rows must not overwrite event 0's)
         self.work = [torch.empty((nws + 15) // 16 * 4, device=dev, dtype=torch.float32) for _ in range(E + 1)]
         self.info = (ctypes.c_int * (2 * E + 2))()
         self.stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
         self._build(E)
-        self._build_halves(E, nws)
 
     def _build(self, E):
         L, B, G, K, C = self.L, self.B, self.G, self.K, self.C
@@ -175,139 +175,37 @@ class LiteralStep:
         self.finalize_args = None
         bwd.append(("event_finalize", self._finalize, (), 0))
         self.fwd, self.bwd = fwd, bwd
+        self.bwd_chain = self._chain(bwd[:-1])
+        self.bwd_run = self.bwd_chain
         self.bytes_fwd = sum(c[3] for c in fwd)
         self.bytes_bwd = sum(c[3] for c in bwd)
 
-    def _build_halves(self, E, nws):
-        """The same step as two half-batch chains on two HIP streams (default priority).
-        Samples are independent through every per-event kernel (and through attention /
-        MLP bodies, which mix tokens only within a sample), so half h runs the whole
-        forward and backward of its batch rows on its own stream and each kernel's ragged
-        last round overlaps the other stream's launches. Every sample's bytes are the same
-        as in the one-stream step. Each event's weight-gradient partial rows of half 1 are
-        placed right after those of half 0 in one workspace (its chunk count is known on
-        the host when the half-0 call returns), so the one deferred finalize sums both
-        halves in a fixed order."""
-        torch = self.torch
-        L, B, G, K, C, S = self.L, self.B, self.G, self.K, self.C, self.S
-        if B % 2:
-            self.halves = None
-            return
+    def use_chain(self, chain: bool) -> None:
+        """Backward launches of step(): chained finalizes, or one deferred finalize."""
+        self.bwd_run = self.bwd_chain if chain else self.bwd
+
+    def _chain(self, partial_calls):
+        """The same backward launches as sihc_event_backward_chain calls: each finalizes the
+        previous call's partial rows in its trailing blocks, so only the last call (slot E,
+        the first read's adjoint) needs a finalize launch of its own."""
+        E, L = self.E, self.L
         vp = ctypes.c_void_p
-        Bh = B // 2
-        car_off = Bh * (G * K) * (G * K) * C * ELEM
-        ws_off = Bh * G * G * C * ELEM
-        nwh = L.sihc_event_backward_workspace_size(Bh, G, K, C)
-        row_bytes = 2 * S * C * 4
-        # one buffer per deferred call holding both halves' partial rows
-        self.work2 = [torch.empty((2 * nwh + 15) // 16 * 4, device=self.x[0].device, dtype=torch.float32)
-                      for _ in range(E + 1)]
-        self.info_h = [(ctypes.c_int * (2 * E + 2))() for _ in range(2)]
-        self.info2 = (ctypes.c_int * (2 * E + 2))()
-        self.streams2 = [torch.cuda.Stream(self.x[0].device) for _ in range(2)]
-        handles = [vp(st.cuda_stream) for st in self.streams2]
-        bf16 = 1
-
-        def car(t, h):
-            return vp(t.data_ptr() + h * car_off)
-
-        def wsp(t, h):
-            return vp(t.data_ptr() + h * ws_off)
-
-        def info(h, k):
-            return ctypes.cast(ctypes.addressof(self.info_h[h]) + 8 * k, ctypes.POINTER(ctypes.c_int))
-
-        def bwd_call(h, k, args):
-            # args: the 14 tensor/size arguments before the workspace; slot k of info / work2
-            def call():
-                base = self.work2[k].data_ptr()
-                off = 0 if h == 0 else self.info_h[0][2 * k] * row_bytes
-                return L.sihc_event_backward_partial(*args, bf16, bf16, vp(base + off), self.work2[k].numel() * 4 - off,
-                                                     info(h, k), handles[h])
-            return call
-
-        halves = []
-        for h in range(2):
-            st = handles[h]
-            calls = []
-            outs = (vp * 1)(self.z[0].data_ptr() + h * ws_off)
-            calls.append(lambda outs=outs, h=h, st=st: L.sihc_read(car(self.x[0], h), vp(self.alpha[0].data_ptr()),
-                                                                   outs, 1, Bh, G, K, C, None, bf16, st))
-            for i in range(E):
-                last = i == E - 1
-                calls.append(lambda i=i, last=last, h=h, st=st: L.sihc_event_forward(
-                    car(self.x[i], h), wsp(self.dz[i], h), vp(self.beta[i].data_ptr()),
-                    None if last else vp(self.alpha[i + 1].data_ptr()), car(self.x[i + 1], h),
-                    None if last else wsp(self.z[i + 1], h), Bh, G, K, C, None, bf16, st))
-            hh = self.h_out
-            calls.append(bwd_call(h, E - 1, (car(hh, h), None, None, wsp(self.dz[E - 1], h),
-                                             vp(self.beta[E - 1].data_ptr()), None, None, wsp(self.gdz[E - 1], h),
-                                             vp(self.gbeta[E - 1].data_ptr()), None, Bh, G, K, C, None)))
-            for i in range(E - 2, -1, -1):
-                dst = self.gx[i % 2]
-                calls.append(bwd_call(h, i, (car(hh, h), wsp(self.gz[i + 1], h), car(self.x[i + 1], h),
-                                             wsp(self.dz[i], h), vp(self.beta[i].data_ptr()),
-                                             vp(self.alpha[i + 1].data_ptr()), car(dst, h), wsp(self.gdz[i], h),
-                                             vp(self.gbeta[i].data_ptr()), vp(self.galpha[i + 1].data_ptr()),
-                                             Bh, G, K, C, None)))
-                hh = dst
-            dst = self.gx[1] if hh is self.gx[0] else self.gx[0]
-            calls.append(bwd_call(h, E, (car(hh, h), wsp(self.gz[0], h), car(self.x[0], h), None, None,
-                                         vp(self.alpha[0].data_ptr()), car(dst, h), None, None,
-                                         vp(self.galpha[0].data_ptr()), Bh, G, K, C, None)))
-            halves.append(calls)
-        self.halves = halves
-
-    def _finalize2(self, slots, stream):
-        """sihc_event_finalize of the listed deferred slots (both halves' partial rows)."""
-        E = self.E
-        for k in slots:
-            c0, r0 = self.info_h[0][2 * k], self.info_h[0][2 * k + 1]
-            c1, r1 = self.info_h[1][2 * k], self.info_h[1][2 * k + 1]
-            assert r0 == r1, "the halves ran different parts"
-            self.info2[2 * k], self.info2[2 * k + 1] = c0 + c1, r0
-        key = tuple(slots)
-        if key not in self.finalize2_args:
-            gb = [self.gbeta[i] for i in range(E)] + [None]
-            ga = [self.galpha[i + 1] for i in range(E - 1)] + [None, self.galpha[0]]
-            ptrs = lambda ts: (ctypes.c_void_p * len(ts))(*(None if t is None else t.data_ptr() for t in ts))  # noqa
-            info = (ctypes.c_int * (2 * len(slots)))()
-            self.finalize2_args[key] = (info, (len(slots), ptrs([self.work2[k] for k in slots]), info,
-                                               ptrs([gb[k] for k in slots]), ptrs([ga[k] for k in slots]),
-                                               self.K, self.C, 1))
-        info, args = self.finalize2_args[key]
-        for j, k in enumerate(slots):
-            info[2 * j], info[2 * j + 1] = self.info2[2 * k], self.info2[2 * k + 1]
-        self.check(self.L.sihc_event_finalize(*args, ctypes.c_void_p(stream.cuda_stream)))
-
-    def step2(self):
-        """One fwd+bwd step as two half-batch streams. The deferred finalize of the events
-        both halves have passed by the middle of the backward runs on a third stream,
-        overlapping the rest of the backward; the remaining events are finalized on the
-        launch stream after both halves end."""
-        torch = self.torch
-        main = torch.cuda.current_stream()
-        if not hasattr(self, "fin_stream"):
-            self.fin_stream = torch.cuda.Stream(self.x[0].device)
-            self.finalize2_args = {}
-        for st in self.streams2:
-            st.wait_stream(main)
-        E = self.E
-        # call positions: read, E forward events, then the backward of slot E - 1, of slots
-        # E - 2 .. 0, and of slot E (the first read's adjoint)
-        mid_slot = E // 2
-        mid_pos = (E + 1) + (E - 1 - mid_slot)
-        for pos, (a, b) in enumerate(zip(*self.halves)):  # interleaved: both streams get work early
-            self.check(a())
-            self.check(b())
-            if pos == mid_pos:
-                for st in self.streams2:
-                    self.fin_stream.wait_stream(st)
-                self._finalize2(list(range(mid_slot, E)), self.fin_stream)
-        for st in self.streams2:
-            main.wait_stream(st)
-        self._finalize2(list(range(mid_slot)) + [E], main)
-        main.wait_stream(self.fin_stream)
+        gb = [self.gbeta[i] for i in range(E)] + [None]
+        ga = [self.galpha[i + 1] for i in range(E - 1)] + [None, self.galpha[0]]
+        slots = [E - 1] + list(range(E - 2, -1, -1)) + [E]  # slot of each backward call, in call order
+        info = lambda k: ctypes.cast(ctypes.addressof(self.info) + 8 * k, ctypes.POINTER(ctypes.c_int))  # noqa: E731
+        p = lambda t: None if t is None else vp(t.data_ptr())  # noqa: E731
+        calls = []
+        for j, (name, _, args, nbytes) in enumerate(partial_calls):
+            prev = (None, None, None, None) if j == 0 else \
+                (p(self.work[slots[j - 1]]), info(slots[j - 1]), p(gb[slots[j - 1]]), p(ga[slots[j - 1]]))
+            calls.append((name, L.sihc_event_backward_chain, args[:-1] + prev + (args[-1],), nbytes))
+        last = slots[-1]
+        ptrs = lambda ts: (vp * len(ts))(*(None if t is None else t.data_ptr() for t in ts))  # noqa: E731
+        fin = (1, ptrs([self.work[last]]), info(last), ptrs([gb[last]]), ptrs([ga[last]]), self.K, self.C, 1,
+               self.stream)
+        calls.append(("event_finalize", L.sihc_event_finalize, fin, 0))
+        return calls
 
     def _finalize(self):
         """sihc_event_finalize over the E + 1 deferred backward calls: slot i < E holds
@@ -381,12 +279,12 @@ class LiteralStep:
         each add a marker packet and an idle gap of several microseconds to the step."""
         if marks is None:
             self.run(self.fwd)
-            self.run(self.bwd)
+            self.run(self.bwd_run)
             return
         ev = lambda: self.torch.cuda.Event(enable_timing=True)  # noqa: E731
         f0, f1, fe, b0, b1 = ev(), ev(), ev(), ev(), ev()
         fh, fb, ft = self.spans(self.fwd, "event_forward")
-        bh, bb, bt = self.spans(self.bwd, "event_backward")
+        bh, bb, bt = self.spans(self.bwd_run, "event_backward")
         self.run(fh)
         f0.record()
         self.run(fb)
@@ -563,9 +461,14 @@ def extra_configs(seed: int) -> dict:
     t_b = _timed(torch, lambda: launch.event_backward(h, gz, xo, d, bw, aw, index=idx))
     t_g = _timed(torch, lambda: launch.gather_cells(x, idx, S))
     t_s = _timed(torch, lambda: launch.scatter_cells(cells, idx))
+    # the same calls without the index, for the cost of the index at this batch
+    t_fu = _timed(torch, lambda: launch.event_forward(x, d, bw, aw))
+    t_bu = _timed(torch, lambda: launch.event_backward(h, gz, xo, d, bw, aw))
     out["config3_indexed"] = {
         "workload": "batch 128, D=1152, int32 state index (seeded groups of 5), bf16",
         "event_forward_GB/s": round(10 * U / t_f / 1e9, 1), "event_backward_GB/s": round(15 * U / t_b / 1e9, 1),
+        "unindexed_event_forward_GB/s": round(10 * U / t_fu / 1e9, 1),
+        "unindexed_event_backward_GB/s": round(15 * U / t_bu / 1e9, 1),
         "gather_GB/s": round(2 * S * U / t_g / 1e9, 1), "scatter_GB/s": round(2 * S * U / t_s / 1e9, 1),
         "event_fwd_bwd_tokens_per_s": round(B * 256 / (t_f + t_b), 1),
     }
@@ -1099,11 +1002,9 @@ def main():
     print(f"[bench] building step: batch={args.batch} C={args.channels} events={args.events}", file=sys.stderr,
           flush=True)
     step = LiteralStep(args.batch, args.channels, args.events, args.seed)
-    two = args.streams == 2
-    if two and step.halves is None:
-        print("--streams 2 needs an even batch", file=sys.stderr)
-        sys.exit(2)
-    run_step = step.step2 if two else (step.step_overlap if args.overlap_finalize else step.step)
+    overlap = args.finalize == "overlap"
+    step.use_chain(args.finalize == "chain")
+    run_step = step.step_overlap if overlap else step.step
     torch.cuda.synchronize()
     for _ in range(args.warmup):
         run_step()
@@ -1111,10 +1012,10 @@ def main():
     print(f"[bench] warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
 
     # Timed region: the K steps back to back, bracketed by device synchronisation. Inside
-    # each one-stream step HIP events mark only the step's phase boundaries and the two
-    # runs of full per-event launches (for the dominant kernels' average launch time).
-    # Two-stream steps overlap launches, so those marks come from one-stream steps run
-    # after the timed region.
+    # each step HIP events mark only the step's phase boundaries and the two runs of full
+    # per-event launches (for the dominant kernels' average launch time). Steps with a
+    # second stream overlap launches, so those marks come from one-stream steps run after
+    # the timed region.
     marks: list = []
     t_fwd: list = []
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
@@ -1123,9 +1024,7 @@ def main():
     for _ in range(args.steps):
         a, c = ev(), ev()
         a.record()
-        if two:
-            step.step2()
-        elif args.overlap_finalize:
+        if overlap:
             step.step_overlap()
         else:
             step.step(marks)
@@ -1136,7 +1035,7 @@ def main():
     ms_step = wall / args.steps * 1e3
     step_ms = statistics.median(a.elapsed_time(c) for a, c in t_fwd)
     one_stream_ms = None
-    if two or args.overlap_finalize:
+    if overlap:
         t_one = []
         for _ in range(max(2, min(args.steps, 5))):
             a, c = ev(), ev()
@@ -1182,8 +1081,10 @@ def main():
             "batch": args.batch, "tokens": 256, "slots": 4, "channels": args.channels,
             "events": args.events, "schedule": "per-event fused (write+read, one carrier pass per event)",
             "parallelism": "single GPU",
-            "streams": ("two half-batch chains (128 images each) on two HIP streams, one deferred finalize"
-                        if two else "one"),
+            "finalize": {"chain": "each backward launch finalizes the previous event's weight gradients in its "
+                                  "trailing blocks (sihc_event_backward_chain)",
+                         "deferred": "one deferred finalize launch per 32 events after the last event",
+                         "overlap": "deferred finalize, half of it on a second stream"}[args.finalize],
         },
         "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(args.batch * 256 / (ms_step * 1e-3), 1),
@@ -1194,8 +1095,10 @@ def main():
         "one_stream_step_ms": None if one_stream_ms is None else round(one_stream_ms, 3),
         "algorithmic_bytes_per_step": total_bytes,
         "roofline": {
-            "kernel": "k_event_bwd (sihc_event_backward_partial, full event; the step's one deferred "
-                      "finalize of all events is outside the launch)",
+            "kernel": ("k_event_bwd (sihc_event_backward_chain, full event, with the previous event's "
+                       "weight-gradient finalize in its trailing blocks)") if args.finalize == "chain" else
+                      ("k_event_bwd (sihc_event_backward_partial, full event; the step's deferred finalize of "
+                       "all events is outside the launch)"),
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

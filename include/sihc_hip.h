@@ -39,7 +39,7 @@ extern "C" {
 #endif
 
 #define SIHC_MAX_EVENTS 32
-#define SIHC_ABI_VERSION 3
+#define SIHC_ABI_VERSION 4
 /* Bytes of the per-GPU scratch array of sihc_event_backward_noalloc (64 MiB). */
 #define SIHC_SCRATCH_BYTES (64u << 20)
 
@@ -163,6 +163,27 @@ int sihc_event_backward_partial(const void *grad_x_out, const void *grad_z_out,
                                 int cell, int channels, const int32_t *index, int dtype,
                                 int w_dtype, void *workspace, size_t workspace_bytes, int *info,
                                 void *stream);
+/* sihc_event_backward_partial for this event, whose launch also runs the deferred
+ * finalize of ONE earlier sihc_event_backward_partial / _chain call in its trailing
+ * blocks: they are dispatched after every block of this event's backward and run while
+ * its last round of blocks drains, so a chain of events needs no finalize launch except
+ * for its last event. prev_workspace / prev_info / prev_grad_beta / prev_grad_alpha_next
+ * are that call's workspace, info and gradients (a gradient its info does not list may be
+ * NULL); it must have used the same cell, channels and dtype, and its launch must precede
+ * this one on `stream` (or have completed). prev_workspace must not overlap `workspace`,
+ * nor its gradients this call's gradients or workspace (checked: SIHC_ERR_INVALID); two
+ * workspaces used in turn suffice for a chain. prev_workspace == NULL: exactly
+ * sihc_event_backward_partial. Same fixed-order sums, so the same bits, as
+ * sihc_event_finalize and sihc_event_backward.
+ * No reference counterpart (a launch schedule of the per-event backward). */
+int sihc_event_backward_chain(const void *grad_x_out, const void *grad_z_out,
+                              const void *x_out, const void *dz, const void *beta,
+                              const void *alpha_next, void *grad_x, void *grad_dz,
+                              void *grad_beta, void *grad_alpha_next, int64_t batch, int grid,
+                              int cell, int channels, const int32_t *index, int dtype,
+                              int w_dtype, void *workspace, size_t workspace_bytes, int *info,
+                              const void *prev_workspace, const int *prev_info,
+                              void *prev_grad_beta, void *prev_grad_alpha_next, void *stream);
 /* The deferred finalizes of n sihc_event_backward_partial calls (host arrays of n
  * workspaces, 2n info ints and n gradient pointers each, as passed to those calls; a
  * gradient the info does not list may be NULL): the fixed-order partial sums of each

@@ -72,11 +72,17 @@
 #ifndef SIHC_EV_MINW  // occupancy hint (min waves per SIMD) of the per-event kernels
 #define SIHC_EV_MINW 1
 #endif
-#ifndef SIHC_EV_CHUNK  // tokens per reduction chunk, per-event backward
-#define SIHC_EV_CHUNK 128
+#ifndef SIHC_EV_CHUNK  // tokens per reduction chunk, per-event backward (4-slot cells)
+#define SIHC_EV_CHUNK 64
 #endif
-#ifndef SIHC_EV_MAXCHUNKS  // most reduction chunks (partial rows) of the per-event backward
+#ifndef SIHC_EV_MAXCHUNKS  // most reduction chunks (partial rows) of the per-event backward (4-slot cells)
 #define SIHC_EV_MAXCHUNKS 1024
+#endif
+#ifndef SIHC_EV_CHUNK_K4  // the same for 16-slot cells, whose partial rows are 4x larger per chunk
+#define SIHC_EV_CHUNK_K4 256
+#endif
+#ifndef SIHC_EV_MAXCHUNKS_K4
+#define SIHC_EV_MAXCHUNKS_K4 512
 #endif
 #ifndef SIHC_EV_GROUP  // tokens per interleaved group of a backward chunk (0: contiguous)
 #define SIHC_EV_GROUP 32
@@ -408,10 +414,12 @@ struct PtrPack {
 // Kernels whose slice rows are whole lines keep the plain order, which measured
 // faster for the 4-slot per-event kernels. A bijection on [0, n) whatever the actual
 // placement, so only speed depends on the round-robin.
+// logical_block_of(n): the same order over the first n blocks of the grid (blocks past
+// them do other work).
 template <bool XCD>
-__device__ __forceinline__ int logical_block() {
+__device__ __forceinline__ int logical_block_of(int n) {
   if constexpr (XCD && SIHC_XCD_MAP) {
-    const int n = int(gridDim.x), b = int(blockIdx.x);
+    const int b = int(blockIdx.x);
     const int q = n >> 3, r = n & 7;  // XCDs 0..r-1 run q+1 blocks, the others q
     const int x = b & 7, i = b >> 3;
     return x < r ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
@@ -419,18 +427,29 @@ __device__ __forceinline__ int logical_block() {
     return int(blockIdx.x);
   }
 }
+template <bool XCD>
+__device__ __forceinline__ int logical_block() {
+  return logical_block_of<XCD>(int(gridDim.x));
+}
 
 // Carrier pixel of slot 0 of the cell token m reads/writes. Token m = b*GG + n owns
 // cell n of batch b, or cell index[m] in the spatially indexed variant.
-__device__ __forceinline__ int64_t cell_pixel0(int m, const Geo& g, const int32_t* __restrict__ index) {
+// cell_pixel0_at: the same with the cell already known (`cell` = the clamped index[m]
+// when `indexed`, ignored otherwise), for kernels that load the index ahead of use.
+__device__ __forceinline__ int64_t cell_pixel0_at(int m, uint32_t cell, bool indexed, const Geo& g) {
   const uint32_t b = fast_div(uint32_t(m), g.divGG);
-  uint32_t n = uint32_t(m) - b * uint32_t(g.GG);
-  // Out-of-range indices (rejected by the host wrappers) are clamped so that no access
-  // can leave the carrier.
-  if (index) n = min(uint32_t(index[m]), uint32_t(g.GG) - 1u);
+  const uint32_t n = indexed ? cell : uint32_t(m) - b * uint32_t(g.GG);
   const uint32_t wy = fast_div(n, g.divG);
   const uint32_t wx = n - wy * uint32_t(g.G);
   return (int64_t(b) * g.GK + int64_t(wy) * g.K) * g.GK + int64_t(wx) * g.K;
+}
+// Out-of-range indices (rejected by the host wrappers) are clamped so that no access can
+// leave the carrier.
+__device__ __forceinline__ uint32_t index_cell(int m, const Geo& g, const int32_t* __restrict__ index) {
+  return min(uint32_t(index[m]), uint32_t(g.GG) - 1u);
+}
+__device__ __forceinline__ int64_t cell_pixel0(int m, const Geo& g, const int32_t* __restrict__ index) {
+  return cell_pixel0_at(m, index ? index_cell(m, g, index) : 0u, index != nullptr, g);
 }
 
 // Element offset of (pixel0 + slot s) at channel c, s = uy*K + ux.
@@ -1841,14 +1860,18 @@ __global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgradz_d2(const bf16_t*
 // lanes then read 512 contiguous bytes per row instead of 128); the sums, and so the
 // bits, do not depend on NV.
 // ----------------------------------------------------------------------------------
+// Block of 256 threads (`tid` = flat thread index); `red` holds FINALIZE_LDS floats of LDS.
+#define FINALIZE_FO 32  // output lanes of a block (each NV outputs)
+#define FINALIZE_FG 8   // chunk groups of a block
+#define FINALIZE_LDS(NV) (FINALIZE_FG * FINALIZE_FO * (NV))
 template <typename TO, int NV>
 __device__ __forceinline__ void finalize_outputs(const float* __restrict__ part, TO* __restrict__ out0,
                                                  TO* __restrict__ out1, int chunks, int R, int S, int C, int pair,
-                                                 int zero_mask, int block) {
-  constexpr int FO = 32, FG = 8;
-  __shared__ float red[FG][FO * NV];
+                                                 int zero_mask, int block, float* __restrict__ lds, int tid) {
+  constexpr int FO = FINALIZE_FO, FG = FINALIZE_FG;
+  float(*red)[FO * NV] = reinterpret_cast<float(*)[FO * NV]>(lds);  // [FG][FO * NV]
   const int64_t n = int64_t(R) * S * C, SC = int64_t(S) * C;  // NV > 1: SC % NV == 0
-  const int o = threadIdx.x % FO, grp = threadIdx.x / FO;
+  const int o = tid % FO, grp = tid / FO;
   const int64_t i = (int64_t(block) * FO + o) * NV;  // this thread's first output
   const bool live = i < n;
   const int r = live ? int(i / SC) : 0;  // the NV outputs share the row r
@@ -1897,7 +1920,9 @@ template <typename TO, int NV>
 __global__ void __launch_bounds__(256) k_finalize(const float* __restrict__ part, TO* __restrict__ out0,
                                                   TO* __restrict__ out1, int chunks, int R, int S, int C,
                                                   int pair, int zero_mask) {
-  finalize_outputs<TO, NV>(part, out0, out1, chunks, R, S, C, pair, zero_mask, int(blockIdx.x));
+  __shared__ float red[FINALIZE_LDS(NV)];
+  finalize_outputs<TO, NV>(part, out0, out1, chunks, R, S, C, pair, zero_mask, int(blockIdx.x), red,
+                           int(threadIdx.x));
 }
 
 // The per-event backward's finalize for up to SIHC_FINALIZE_BATCH deferred events in one
@@ -1916,8 +1941,33 @@ struct FinalizeBatch {
 template <typename TO>
 __global__ void __launch_bounds__(256) k_finalize_batch(FinalizeBatch b, int S, int C) {
   const int e = int(blockIdx.y);
+  __shared__ float red[FINALIZE_LDS(4)];
   finalize_outputs<TO, 4>(b.part[e], static_cast<TO*>(b.out0[e]), static_cast<TO*>(b.out1[e]), b.chunks[e], 2, S, C,
-                          1, b.zero_mask[e], int(blockIdx.x));
+                          1, b.zero_mask[e], int(blockIdx.x), red, int(threadIdx.x));
+}
+
+// The deferred finalize of one earlier per-event backward call, run by the trailing
+// blocks of a later per-event backward launch (sihc_event_backward_chain): blocks
+// nmain, nmain + 1, ... of that grid are dispatched after every block of the backward
+// proper, so they run while its last round of blocks drains. Same fixed-order sums
+// (finalize_outputs, 4 outputs per thread) as k_finalize_batch, so the same bits.
+struct EvCarry {
+  const float* part;  // the earlier call's partial rows [chunks][2][S][C] (NULL: none)
+  void* out0;         // its grad_beta [C][S] (NULL: row 0 not stored)
+  void* out1;         // its grad_alpha_next [C][S] (NULL: row 1 not stored)
+  int chunks;         // its partial-row count
+  int zero_mask;      // rows stored as zeros without reading partials
+  int nmain;          // blocks of the launch's own backward; blocks from here on finalize
+};
+#define EV_CARRY_OUTPUTS_PER_BLOCK (FINALIZE_FO * 4)
+
+template <typename T>
+__device__ __forceinline__ bool run_carry(const EvCarry& carry, int S, int C, float* lds) {
+  if (int(blockIdx.x) < carry.nmain) return false;
+  finalize_outputs<T, 4>(carry.part, static_cast<T*>(carry.out0), static_cast<T*>(carry.out1), carry.chunks, 2, S, C,
+                         1, carry.zero_mask, int(blockIdx.x) - carry.nmain, lds,
+                         int(threadIdx.y * blockDim.x + threadIdx.x));
+  return true;
 }
 
 template <typename TO>
@@ -2163,13 +2213,14 @@ __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_bwd(const T* __rest
                                                    const T* __restrict__ alpha, T* __restrict__ gx,
                                                    T* __restrict__ gdz, float* __restrict__ part,
                                                    const int32_t* __restrict__ index, Geo g, int gs, int nchunks,
-                                                   int nslices) {
+                                                   int nslices, EvCarry carry) {
   constexpr int S = K * K;
   constexpr int U = SIHC_EV_UNROLL;  // tokens per lane per iteration
-  extern __shared__ float red[];
+  extern __shared__ float red[];  // TL x BCG x S x V floats (>= FINALIZE_LDS(4): 256 x 4)
+  if (run_carry<T>(carry, S, g.C, red)) return;
   const int BCG = blockDim.x, TL = blockDim.y;
   const int BC = BCG * V;
-  const int blk = logical_block<K == 4>(), slice = blk % nslices, chunk = blk / nslices;
+  const int blk = logical_block_of<K == 4>(carry.nmain), slice = blk % nslices, chunk = blk / nslices;
   const int c0 = slice * BC + threadIdx.x * V;
   float db[S][V], da[S][V];
 #pragma unroll
@@ -2230,19 +2281,42 @@ __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_bwd(const T* __rest
         if constexpr (HAS_W) store_vec<T, V, NTS>(gdz + zoff, gd);
       }
     };
-    for (int64_t m0 = int64_t(chunk) * gs; m0 < M; m0 += int64_t(nchunks) * gs) {
+    // With a state index, the cells of an iteration's tokens are loaded one iteration
+    // ahead, so its carrier addresses do not wait on an index load (an unhidden dependent
+    // load per iteration cost the indexed backward 8% at 2 waves per SIMD).
+    const int64_t gstride = int64_t(nchunks) * gs;
+    uint32_t cell_next[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) cell_next[u] = 0u;
+    auto fetch_cells = [&](int64_t mi, int64_t m_end) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t mt = mi + threadIdx.y + u * TL;
+        cell_next[u] = index_cell(int(mt < m_end ? mt : mi), g, index);
+      }
+    };
+    if (index && int64_t(chunk) * gs < M) fetch_cells(int64_t(chunk) * gs, min(int64_t(chunk) * gs + gs, M));
+    for (int64_t m0 = int64_t(chunk) * gs; m0 < M; m0 += gstride) {
       const int64_t m_end = min(m0 + gs, M);
       for (int64_t mi = m0; mi < m_end; mi += U * TL) {
         int64_t p0[U], zoff[U];
         bool ok[U];
         float gz[U][V], d[U][V], t[U][S][V], xv[U][S][V];
+        uint32_t cell[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) cell[u] = cell_next[u];
+        if (index) {  // the next iteration: this group's next rows, or the chunk's next group
+          const bool same = mi + U * TL < m_end;
+          const int64_t mn = same ? mi + U * TL : m0 + gstride;
+          if (mn < M) fetch_cells(mn, same ? m_end : min(mn + gs, M));
+        }
         // loads (tail tokens reload the iteration's first token, which is valid)
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           const int64_t mt = mi + threadIdx.y + u * TL;
           ok[u] = mt < m_end;
           const int mu = int(ok[u] ? mt : mi);
-          p0[u] = cell_pixel0(mu, g, index);
+          p0[u] = cell_pixel0_at(mu, cell[u], index != nullptr, g);
           zoff[u] = int64_t(mu) * g.C + c0;
           if constexpr (HAS_G) load_vec<T, V, NTL>(gzo + zoff[u], gz[u]);
           if constexpr (HAS_W) load_vec<T, V, NTL>(dz + zoff[u], d[u]);
@@ -2305,12 +2379,13 @@ __global__ void __launch_bounds__(256, SIHC_EV16_MINW) k_event_bwd16(const bf16_
                                                      const bf16_t* __restrict__ alpha, bf16_t* __restrict__ gx,
                                                      bf16_t* __restrict__ gdz, float* __restrict__ part,
                                                      const int32_t* __restrict__ index, Geo g, int gs, int nchunks,
-                                                     int nslices) {
+                                                     int nslices, EvCarry carry) {
   constexpr int K = 4, S = 16, V = 2;
-  extern __shared__ float red[];
+  extern __shared__ float red[];  // TL x BCG x S x V floats (>= FINALIZE_LDS(4))
+  if (run_carry<bf16_t>(carry, S, g.C, red)) return;
   const int BCG = blockDim.x, TL = blockDim.y;
   const int BC = BCG * V;
-  const int blk = logical_block<true>(), slice = blk % nslices, chunk = blk / nslices;
+  const int blk = logical_block_of<true>(carry.nmain), slice = blk % nslices, chunk = blk / nslices;
   const int c0 = slice * BC + threadIdx.x * V;
   float db[S][V], da[S][V];
 #pragma unroll
@@ -2657,10 +2732,12 @@ int wgrad_chunks(int64_t M, int events, int C) {
 }
 // Reduction chunks of the per-event backward: 4-slot cells one per SIHC_EV_CHUNK tokens up
 // to SIHC_EV_MAXCHUNKS; 16-slot cells, whose partial rows are 4x larger per chunk, one per
-// 2 x SIHC_EV_CHUNK tokens up to half as many.
+// SIHC_EV_CHUNK_K4 tokens up to SIHC_EV_MAXCHUNKS_K4. At the benchmark shape (65,536 tokens,
+// 4 slots) 1,024 chunks of 64 tokens: blocks of ~20 us whose ragged last round costs less
+// than the 128-token chunks' (380 vs 383 us per event with the chained finalize).
 int event_bwd_chunks(int64_t M, int cell) {
   return cell == 2 ? chunk_count(M, SIHC_EV_CHUNK, SIHC_EV_MAXCHUNKS)
-                   : chunk_count(M, 2 * SIHC_EV_CHUNK, SIHC_EV_MAXCHUNKS / 2);
+                   : chunk_count(M, SIHC_EV_CHUNK_K4, SIHC_EV_MAXCHUNKS_K4);
 }
 // Token chunks of the fused triangular backward (which also stores the update
 // gradients): one per SIHC_TRIB_CHUNK tokens up to 1024, at least the weight-gradient
@@ -3560,7 +3637,8 @@ static int event_backward_impl(const char* what, const void* grad_x_out, const v
                                const void* dz, const void* beta, const void* alpha_next, void* grad_x, void* grad_dz,
                                void* grad_beta, void* grad_alpha_next, int64_t batch, int grid, int cell,
                                int channels, const int32_t* index, int dtype, int w_dtype, void* workspace,
-                               size_t workspace_bytes, void* stream, int* defer = nullptr) {
+                               size_t workspace_bytes, void* stream, int* defer = nullptr,
+                               const EvCarry* prev = nullptr) {
   Geo g;
   if (int rc = check_geometry(what, batch, grid, cell, channels, &g)) return rc;
   if (!valid_dtype(dtype) || !valid_dtype(w_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
@@ -3571,8 +3649,25 @@ static int event_backward_impl(const char* what, const void* grad_x_out, const v
   const int S = cell * cell;
   const int64_t wn = int64_t(S) * channels;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // an earlier deferred call's finalize, run by this launch's trailing blocks
+  const bool carry = prev && prev->part;
+  const unsigned carry_blocks =
+      carry ? unsigned((int64_t(2) * S * channels + EV_CARRY_OUTPUTS_PER_BLOCK - 1) / EV_CARRY_OUTPUTS_PER_BLOCK) : 0u;
   if (g.M == 0) {  // no tokens: zero weight gradients (token tensors may carry NULL pointers)
     if (defer) defer[0] = defer[1] = 0;  // nothing left for the finalize
+    if (carry) {  // no launch of the backward to carry it: a finalize launch of its own
+      FinalizeBatch b{};
+      b.part[0] = prev->part;
+      b.out0[0] = prev->out0;
+      b.out1[0] = prev->out1;
+      b.chunks[0] = prev->chunks;
+      b.zero_mask[0] = prev->zero_mask;
+      if (w_dtype == SIHC_DTYPE_F32)
+        hipLaunchKernelGGL((k_finalize_batch<float>), dim3(carry_blocks, 1), dim3(256), 0, st, b, S, channels);
+      else
+        hipLaunchKernelGGL((k_finalize_batch<bf16_t>), dim3(carry_blocks, 1), dim3(256), 0, st, b, S, channels);
+      if (int rc = check_launch(what)) return rc;
+    }
     if (beta && grad_beta)
       if (int rc = fill_zero(w_dtype, grad_beta, wn, st, what)) return rc;
     if (grad_alpha_next) return fill_zero(w_dtype, grad_alpha_next, wn, st, what);
@@ -3604,6 +3699,8 @@ static int event_backward_impl(const char* what, const void* grad_x_out, const v
     V /= 2;
   const Shape2D sh = shape_for(channels, V, SIHC_EV_BCG, 0);
   const size_t lds = size_t(sh.tl) * sh.bcg * S * V * sizeof(float);  // TL x (BCG*S*V) floats
+  if (carry && (sh.tl * sh.bcg != 256 || lds < FINALIZE_LDS(4) * sizeof(float)))
+    return fail(SIHC_ERR_INVALID, "%s: internal block shape of the carried finalize", what);
   float* part = static_cast<float*>(workspace);
   const bool store_t = grad_x != nullptr;
   // Valid part combinations: read part present (t stored), or write part only.
@@ -3635,21 +3732,25 @@ static int event_backward_impl(const char* what, const void* grad_x_out, const v
               // group 0 means one contiguous run of tokens per chunk
               const int gs = group_tokens(KK == 2 ? SIHC_EV_GROUP : SIHC_EV_GROUP_K4, g.M, chunks,
                                           SIHC_EV_UNROLL * sh.tl);
+              EvCarry cy{};
+              if (carry) cy = *prev;
+              cy.nmain = int(blocks1d(sh.slices, chunks));
+              const dim3 grid_blocks(blocks1d(sh.slices, chunks) + carry_blocks);
               if constexpr (B16) {
-                hipLaunchKernelGGL((k_event_bwd16<HH, HG, HW, STT, NTL, NTS>), dim3(blocks1d(sh.slices, chunks)),
-                                   dim3(sh.bcg, sh.tl), lds, st, static_cast<const T*>(grad_x_out),
-                                   static_cast<const T*>(grad_z_out), static_cast<const T*>(x_out),
-                                   static_cast<const T*>(dz), static_cast<const T*>(beta),
-                                   static_cast<const T*>(alpha_next), static_cast<T*>(grad_x),
-                                   static_cast<T*>(grad_dz), part, index, g, gs, chunks, sh.slices);
+                hipLaunchKernelGGL((k_event_bwd16<HH, HG, HW, STT, NTL, NTS>), grid_blocks, dim3(sh.bcg, sh.tl), lds,
+                                   st, static_cast<const T*>(grad_x_out), static_cast<const T*>(grad_z_out),
+                                   static_cast<const T*>(x_out), static_cast<const T*>(dz),
+                                   static_cast<const T*>(beta), static_cast<const T*>(alpha_next),
+                                   static_cast<T*>(grad_x), static_cast<T*>(grad_dz), part, index, g, gs, chunks,
+                                   sh.slices, cy);
                 return check_launch(what);
               }
-              hipLaunchKernelGGL((k_event_bwd<T, VV, KK, HH, HG, HW, STT, NTL, NTS>), dim3(blocks1d(sh.slices, chunks)),
-                                 dim3(sh.bcg, sh.tl), lds, st, static_cast<const T*>(grad_x_out),
-                                 static_cast<const T*>(grad_z_out), static_cast<const T*>(x_out),
-                                 static_cast<const T*>(dz), static_cast<const T*>(beta),
-                                 static_cast<const T*>(alpha_next), static_cast<T*>(grad_x), static_cast<T*>(grad_dz),
-                                 part, index, g, gs, chunks, sh.slices);
+              hipLaunchKernelGGL((k_event_bwd<T, VV, KK, HH, HG, HW, STT, NTL, NTS>), grid_blocks, dim3(sh.bcg, sh.tl),
+                                 lds, st, static_cast<const T*>(grad_x_out), static_cast<const T*>(grad_z_out),
+                                 static_cast<const T*>(x_out), static_cast<const T*>(dz),
+                                 static_cast<const T*>(beta), static_cast<const T*>(alpha_next),
+                                 static_cast<T*>(grad_x), static_cast<T*>(grad_dz), part, index, g, gs, chunks,
+                                 sh.slices, cy);
               return check_launch(what);
             };
             switch (mode) {
@@ -3697,6 +3798,61 @@ int sihc_event_backward_partial(const void* grad_x_out, const void* grad_z_out, 
   return event_backward_impl(what, grad_x_out, grad_z_out, x_out, dz, beta, alpha_next, grad_x, grad_dz, grad_beta,
                              grad_alpha_next, batch, grid, cell, channels, index, dtype, w_dtype, workspace,
                              workspace_bytes, stream, info);
+}
+
+// [a, a + na) and [b, b + nb) share a byte
+static bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return na && nb && x < y + nb && y < x + na;
+}
+
+int sihc_event_backward_chain(const void* grad_x_out, const void* grad_z_out, const void* x_out, const void* dz,
+                              const void* beta, const void* alpha_next, void* grad_x, void* grad_dz, void* grad_beta,
+                              void* grad_alpha_next, int64_t batch, int grid, int cell, int channels,
+                              const int32_t* index, int dtype, int w_dtype, void* workspace, size_t workspace_bytes,
+                              int* info, const void* prev_workspace, const int* prev_info, void* prev_grad_beta,
+                              void* prev_grad_alpha_next, void* stream) {
+  const char* what = "sihc_event_backward_chain";
+  if (!info) return fail(SIHC_ERR_INVALID, "%s: null info", what);
+  if (!prev_workspace)  // nothing carried: sihc_event_backward_partial
+    return event_backward_impl(what, grad_x_out, grad_z_out, x_out, dz, beta, alpha_next, grad_x, grad_dz,
+                               grad_beta, grad_alpha_next, batch, grid, cell, channels, index, dtype, w_dtype,
+                               workspace, workspace_bytes, stream, info);
+  if (!prev_info) return fail(SIHC_ERR_INVALID, "%s: null prev_info", what);
+  if (cell != 2 && cell != 4) return fail(SIHC_ERR_INVALID, "%s: cell must be 2 or 4 (4 or 16 slots)", what);
+  if (channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
+  const int chunks = prev_info[0], rows = prev_info[1];
+  if (chunks < 0 || rows < 0 || rows > 3) return fail(SIHC_ERR_INVALID, "%s: bad prev_info", what);
+  const int S = cell * cell;
+  const size_t wbytes = size_t(S) * channels * elem_size(w_dtype);
+  const size_t prev_bytes = size_t(chunks) * 2 * S * channels * sizeof(float);
+  EvCarry cy{};
+  if (chunks > 0 && rows > 0) {
+    if (((rows & 1) && !prev_grad_beta) || ((rows & 2) && !prev_grad_alpha_next))
+      return fail(SIHC_ERR_INVALID, "%s: null gradient of the carried call", what);
+    if (!aligned(prev_workspace, 16)) return fail(SIHC_ERR_INVALID, "%s: prev_workspace must be 16-byte aligned", what);
+    // the trailing blocks read prev_workspace and write the carried gradients while the
+    // backward proper writes its own partial rows and gradients
+    if (overlaps(prev_workspace, prev_bytes, workspace, workspace_bytes))
+      return fail(SIHC_ERR_INVALID, "%s: prev_workspace overlaps this call's workspace", what);
+    const void* mine[] = {grad_beta, grad_alpha_next};
+    const void* theirs[] = {(rows & 1) ? prev_grad_beta : nullptr, (rows & 2) ? prev_grad_alpha_next : nullptr};
+    for (const void* a : mine)
+      for (const void* b : theirs)
+        if (a && b && overlaps(a, wbytes, b, wbytes))
+          return fail(SIHC_ERR_INVALID, "%s: the carried call's gradients overlap this call's", what);
+    for (const void* b : theirs)
+      if (b && overlaps(b, wbytes, workspace, workspace_bytes))
+        return fail(SIHC_ERR_INVALID, "%s: the carried call's gradients overlap this call's workspace", what);
+    cy.part = static_cast<const float*>(prev_workspace);
+    cy.out0 = theirs[0] ? prev_grad_beta : nullptr;
+    cy.out1 = theirs[1] ? prev_grad_alpha_next : nullptr;
+    cy.chunks = chunks;
+    cy.zero_mask = ((rows & 1) ? 0 : 1) | ((rows & 2) ? 0 : 2);  // rows without partials: not read
+  }
+  return event_backward_impl(what, grad_x_out, grad_z_out, x_out, dz, beta, alpha_next, grad_x, grad_dz, grad_beta,
+                             grad_alpha_next, batch, grid, cell, channels, index, dtype, w_dtype, workspace,
+                             workspace_bytes, stream, info, cy.part ? &cy : nullptr);
 }
 
 int sihc_event_finalize(int n, const void* const* workspaces, const int* info, void* const* grad_beta,

@@ -10,7 +10,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libsihc_hip.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 MAX_EVENTS = 32
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -41,6 +41,10 @@ PROTOTYPES: dict[str, tuple] = {
     "sihc_event_backward_partial": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                            _i64, _i32, _i32, _i32, _vp, _i32, _i32, _vp, _sz,
                                            ctypes.POINTER(ctypes.c_int), _vp]),
+    "sihc_event_backward_chain": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                         _i64, _i32, _i32, _i32, _vp, _i32, _i32, _vp, _sz,
+                                         ctypes.POINTER(ctypes.c_int), _vp, ctypes.POINTER(ctypes.c_int),
+                                         _vp, _vp, _vp]),
     "sihc_event_finalize": (_i32, [_i32, _vpp, ctypes.POINTER(ctypes.c_int), _vpp, _vpp, _i32, _i32, _i32, _vp]),
     "sihc_event_backward_noalloc": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                            _i64, _i32, _i32, _i32, _vp, _i32, _i32, _vp]),

@@ -41,7 +41,11 @@ def test_workspace_sizes_are_pure_functions_of_sizes():
     # the query also covers the fused triangular backward: one chunk per 64 tokens, at
     # most 1024 (more than the 152 chunks the 11-update gamma gradient takes)
     assert lib.sihc_triangular_gamma_grad_workspace_size(11, 65536, 1152) == 1024 * 11 * 1152 * 4
-    assert lib.sihc_event_backward_workspace_size(256, 16, 2, 1152) == 512 * 2 * 4 * 1152 * 4
+    # per-event backward: 4-slot cells one chunk per 64 tokens up to 1024, 16-slot cells one
+    # per 256 tokens up to 512
+    assert lib.sihc_event_backward_workspace_size(256, 16, 2, 1152) == 1024 * 2 * 4 * 1152 * 4
+    assert lib.sihc_event_backward_workspace_size(3, 16, 2, 136) == 12 * 2 * 4 * 136 * 4
+    assert lib.sihc_event_backward_workspace_size(256, 16, 4, 1152) == 256 * 2 * 16 * 1152 * 4
 
 
 FAKE = 0x1000  # never dereferenced: every call below fails argument validation first

@@ -136,51 +136,143 @@ def test_event_op_handles_unused_outputs():
     assert torch.equal(gx2, torch.ones_like(gx2))
 
 
-def test_deferred_finalize_matches_per_call_finalize():
+def _finalize_chain_case(dtype, slots, n, seed):
+    """n per-event backward calls (full, write-only and read-only modes in turn; call
+    n // 2 has no tokens) with their per-call results from sihc_event_backward."""
+    torch.manual_seed(seed)
+    b, c = 3, 136
+    k = O.cell_edge(slots)
+    x_out = torch.randn(b, 16 * k, 16 * k, c, device="cuda").to(dtype)
+    dz = torch.randn(b, 256, c, device="cuda").to(dtype)
+    h = 1e-2 * torch.randn_like(x_out)
+    g = 1e-2 * torch.randn_like(dz)
+    empty = [t[:0] for t in (x_out, dz, h, g)]
+    cases = []
+    for i in range(n):
+        beta = (1.0 + 0.05 * torch.randn(c, slots, device="cuda")).to(dtype)
+        alpha = (0.25 + 0.05 * torch.randn(c, slots, device="cuda")).to(dtype)
+        xo, d, hh, gg = empty if i == n // 2 else (x_out, dz, h, g)
+        mode = ("full", "write", "read")[i % 3]
+        args = dict(full=(hh, gg, xo, d, beta, alpha), write=(hh, None, None, d, beta, None),
+                    read=(hh, gg, xo, None, None, alpha))[mode]
+        ref = launch.event_backward(*args, carrier_like=xo)
+        cases.append((mode, xo.shape[0], args, ref))
+    return cases, c, k
+
+
+def _run_partial(L, entry, case, c, k, code, work, info_slot, prev, st):
+    import ctypes
+
+    p = lambda t: None if t is None or t.numel() == 0 else ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    mode, b, args, ref = case
+    outs = [torch.full_like(t, float("nan")) if t is not None else None for t in ref]
+    gx = outs[0] if mode != "write" else torch.full_like(ref[0], float("nan"))
+    hh, gz, xo, d, bt, al = args
+    call = (p(hh), p(gz), p(xo), p(d), p(bt), p(al), p(gx), p(outs[1]), p(outs[2]), p(outs[3]), b, 16, k, c, None,
+            code, code, ctypes.c_void_p(work.data_ptr()), work.numel() * 4, info_slot)
+    if entry == "chain":
+        _lib_check(L.sihc_event_backward_chain(*call, *prev, st))
+    else:
+        _lib_check(L.sihc_event_backward_partial(*call, st))
+    return (gx, *outs[1:])
+
+
+def _lib_check(rc):
+    from sihc_hip import _lib
+
+    _lib.check(rc)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("slots", [4, 16])
+def test_deferred_finalize_matches_per_call_finalize(dtype, slots):
     # sihc_event_backward_partial over a chain of 35 events (full, write-only and read-only
-    # modes), then one sihc_event_finalize (two launches: 32 + 3 events): every output
-    # bit-identical to sihc_event_backward's own finalize.
+    # modes; one event without tokens), then one sihc_event_finalize (two launches: 32 + 3
+    # events): every output bit-identical to sihc_event_backward's own finalize.
     import ctypes
 
     from sihc_hip import _lib
 
-    announce("deferred event finalize, 35 events")
-    torch.manual_seed(41)
+    announce(f"deferred event finalize, 35 events, {dtype}, {slots} slots")
     L = _lib.lib()
-    b, c, slots = 3, 136, 4
-    x_out = torch.randn(b, 32, 32, c, device="cuda").to(torch.bfloat16)
-    dz = torch.randn(b, 256, c, device="cuda").to(torch.bfloat16)
-    h = (1e-2 * torch.randn_like(x_out))
-    g = (1e-2 * torch.randn_like(dz))
-    nws = L.sihc_event_backward_workspace_size(b, 16, 2, c)
-    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
     n = 35
+    cases, c, k = _finalize_chain_case(dtype, slots, n, seed=41)
+    code = _lib.DTYPE_F32 if dtype == torch.float32 else _lib.DTYPE_BF16
+    nws = L.sihc_event_backward_workspace_size(3, 16, k, c)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     info = (ctypes.c_int * (2 * n))()
     slot = lambda i: ctypes.cast(ctypes.addressof(info) + 8 * i, ctypes.POINTER(ctypes.c_int))  # noqa: E731
-    works, got, ref = [], [], []
-    for i in range(n):
-        beta = (1.0 + 0.05 * torch.randn(c, slots, device="cuda")).to(torch.bfloat16)
-        alpha = (0.25 + 0.05 * torch.randn(c, slots, device="cuda")).to(torch.bfloat16)
-        mode = ("full", "write", "read")[i % 3]
-        args = dict(full=(h, g, x_out, dz, beta, alpha), write=(h, None, None, dz, beta, None),
-                    read=(h, g, x_out, None, None, alpha))[mode]
-        ref.append(launch.event_backward(*args, carrier_like=x_out))
-        outs = [torch.full_like(t, float("nan")) if t is not None else None for t in ref[-1]]
-        gx = outs[0] if mode != "write" else torch.full_like(x_out, float("nan"))
-        work = torch.empty(nws // 4 + 16, device="cuda", dtype=torch.float32)
-        works.append(work)
-        hh, gz, xo, d, bt, al = args
-        _lib.check(L.sihc_event_backward_partial(p(hh), p(gz), p(xo), p(d), p(bt), p(al), p(gx), p(outs[1]),
-                                                 p(outs[2]), p(outs[3]), b, 16, 2, c, None, 1, 1, p(work),
-                                                 work.numel() * 4, slot(i), st))
-        got.append((gx, *outs[1:]))
+    works, got = [], []
+    for i, case in enumerate(cases):
+        works.append(torch.empty(nws // 4 + 16, device="cuda", dtype=torch.float32))
+        got.append(_run_partial(L, "partial", case, c, k, code, works[-1], slot(i), None, st))
+    assert info[2 * (n // 2)] == 0, "the call without tokens leaves no partial rows"
     vp = lambda ts: _lib.ptr_array(None if t is None else t.data_ptr() for t in ts)  # noqa: E731
     _lib.check(L.sihc_event_finalize(n, vp(works), info, vp([o[2] for o in got]), vp([o[3] for o in got]),
-                                     2, c, 1, st))
+                                     k, c, code, st))
     torch.cuda.synchronize()
-    for i, (a, r) in enumerate(zip(got, ref)):
-        for k in range(4):
-            if r[k] is None:
+    for i, (a, case) in enumerate(zip(got, cases)):
+        for j in range(4):
+            if case[3][j] is None:
                 continue
-            assert torch.equal(a[k], r[k]), f"event {i} output {k} differs"
+            assert torch.equal(a[j], case[3][j]), f"event {i} output {j} differs"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("slots", [4, 16])
+def test_chained_finalize_matches_per_call_finalize(dtype, slots):
+    # sihc_event_backward_chain over a chain of 13 events with two workspaces used in turn:
+    # each launch finalizes the previous call's partial rows in its trailing blocks (the
+    # call without tokens finalizes its predecessor with a launch of its own), and one
+    # sihc_event_finalize ends the chain. Every output bit-identical to sihc_event_backward.
+    import ctypes
+
+    from sihc_hip import _lib
+
+    announce(f"chained event finalize, 13 events, {dtype}, {slots} slots")
+    L = _lib.lib()
+    n = 13
+    cases, c, k = _finalize_chain_case(dtype, slots, n, seed=43)
+    code = _lib.DTYPE_F32 if dtype == torch.float32 else _lib.DTYPE_BF16
+    nws = L.sihc_event_backward_workspace_size(3, 16, k, c)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    info = (ctypes.c_int * (2 * n))()
+    slot = lambda i: ctypes.cast(ctypes.addressof(info) + 8 * i, ctypes.POINTER(ctypes.c_int))  # noqa: E731
+    works = [torch.full((nws // 4 + 16,), float("nan"), device="cuda") for _ in range(2)]
+    got = []
+    p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    for i, case in enumerate(cases):
+        prev = (None, None, None, None) if i == 0 else \
+            (p(works[(i - 1) % 2]), slot(i - 1), p(got[-1][2]), p(got[-1][3]))
+        got.append(_run_partial(L, "chain", case, c, k, code, works[i % 2], slot(i), prev, st))
+    _lib.check(L.sihc_event_finalize(1, _lib.ptr_array([works[(n - 1) % 2].data_ptr()]), slot(n - 1),
+                                     _lib.ptr_array([None if got[-1][2] is None else got[-1][2].data_ptr()]),
+                                     _lib.ptr_array([None if got[-1][3] is None else got[-1][3].data_ptr()]),
+                                     k, c, code, st))
+    torch.cuda.synchronize()
+    for i, (a, case) in enumerate(zip(got, cases)):
+        for j in range(4):
+            if case[3][j] is None:
+                continue
+            assert torch.equal(a[j], case[3][j]), f"event {i} output {j} differs"
+
+
+def test_chained_finalize_rejects_overlapping_workspaces():
+    import ctypes
+
+    from sihc_hip import _lib
+
+    announce("chained event finalize argument checks")
+    L = _lib.lib()
+    cases, c, k = _finalize_chain_case(torch.bfloat16, 4, 3, seed=3)  # cases[0]: a full event with tokens
+    nws = L.sihc_event_backward_workspace_size(3, 16, k, c)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    info = (ctypes.c_int * 4)()
+    slot = lambda i: ctypes.cast(ctypes.addressof(info) + 8 * i, ctypes.POINTER(ctypes.c_int))  # noqa: E731
+    work = torch.empty(nws // 4 + 16, device="cuda")
+    got = _run_partial(L, "partial", cases[0], c, k, _lib.DTYPE_BF16, work, slot(0), None, st)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    with pytest.raises(_lib.SihcError, match="overlaps this call's workspace"):
+        _run_partial(L, "chain", cases[0], c, k, _lib.DTYPE_BF16, work, slot(1),
+                     (p(work), slot(0), p(got[2]), p(got[3])), st)
+    torch.cuda.synchronize()

@@ -43,4 +43,5 @@ def test_empty_last_chunk_writes_zero_partials(rows, channels, active):
     for j in range(active):
         assert torch.equal(ddz[j].cpu(), rdz[j]), f"update gradient {j} not bit-exact"
     assert torch.isfinite(dg).all(), "a partial row was left unwritten"
-    assert_parity(dg, rdg, torch.bfloat16, what="dgamma", kind="reduced")
+    # fp32 gamma gradient: the fp32 bar against the oracle's float64 sums
+    assert_parity(dg, rdg, torch.float32, what="dgamma")

@@ -77,13 +77,13 @@ def test_noalloc_matches_workspace_entry_point_twice(pair):
 
 
 def test_noalloc_rejects_sizes_beyond_its_scratch():
-    # 16 slots, 65,536 tokens, 4096 channels: 512 chunks x 2 x 16 x 4096 x 4 B = 256 MiB of
-    # partial rows, more than the 64 MiB array; rejected from the sizes alone, before any
-    # HIP call (so this runs without a GPU)
+    # 16 slots, 65,536 tokens, 4096 channels: 256 chunks of 256 tokens x 2 x 16 x 4096 x 4 B
+    # = 128 MiB of partial rows, more than the 64 MiB array; rejected from the sizes alone,
+    # before any HIP call (so this runs without a GPU)
     L = _lib.lib()
     fake = 0x1000
     need = L.sihc_event_backward_workspace_size(256, 16, 4, 4096)
-    assert need > 64 << 20
+    assert need == 256 * 2 * 16 * 4096 * 4 > 64 << 20
     rc = L.sihc_event_backward_noalloc(*([fake] * 10), 256, 16, 4, 4096, None, 1, 1, None)
     assert rc == 1 and b"scratch" in L.sihc_last_error() and b"67108864" in L.sihc_last_error()
     # at the benchmark shape (4 slots, 1152 channels) the partial rows fit
