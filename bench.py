@@ -48,10 +48,9 @@ def parse_args():
     p.add_argument("--channels", type=int, default=1152)
     p.add_argument("--events", type=int, default=56)
     p.add_argument("--seed", type=int, default=2)
-    p.add_argument("--finalize", choices=("chain", "deferred", "overlap"), default="chain",
+    p.add_argument("--finalize", choices=("chain", "deferred"), default="chain",
                    help="weight-gradient finalize of the backward: in the next launch's trailing blocks "
-                        "(sihc_event_backward_chain), one deferred launch per 32 events after the last event, "
-                        "or half of that deferred finalize on a second stream")
+                        "(sihc_event_backward_chain), or one deferred launch per 32 events after the last event")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extra", action="store_true", help="skip the secondary config 1/3/4 figures")
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
@@ -95,6 +94,7 @@ class LiteralStep:
         self.torch = torch
         self.L = _lib.lib()
         self.check = _lib.check
+        self.size_array = _lib.size_array
         dev = torch.device("cuda", 0)
         bf = torch.bfloat16
         g = torch.Generator(device=dev).manual_seed(seed)
@@ -197,13 +197,14 @@ class LiteralStep:
         p = lambda t: None if t is None else vp(t.data_ptr())  # noqa: E731
         calls = []
         for j, (name, _, args, nbytes) in enumerate(partial_calls):
-            prev = (None, None, None, None) if j == 0 else \
-                (p(self.work[slots[j - 1]]), info(slots[j - 1]), p(gb[slots[j - 1]]), p(ga[slots[j - 1]]))
+            k = slots[j - 1]
+            prev = (None, 0, None, None, None) if j == 0 else \
+                (p(self.work[k]), self.work[k].numel() * 4, info(k), p(gb[k]), p(ga[k]))
             calls.append((name, L.sihc_event_backward_chain, args[:-1] + prev + (args[-1],), nbytes))
         last = slots[-1]
         ptrs = lambda ts: (vp * len(ts))(*(None if t is None else t.data_ptr() for t in ts))  # noqa: E731
-        fin = (1, ptrs([self.work[last]]), info(last), ptrs([gb[last]]), ptrs([ga[last]]), self.K, self.C, 1,
-               self.stream)
+        fin = (1, ptrs([self.work[last]]), self.size_array([self.work[last].numel() * 4]), info(last),
+               ptrs([gb[last]]), ptrs([ga[last]]), self.K, self.C, 1, self.stream)
         calls.append(("event_finalize", L.sihc_event_finalize, fin, 0))
         return calls
 
@@ -214,49 +215,11 @@ class LiteralStep:
         if self.finalize_args is None:
             E = self.E
             ptrs = lambda ts: (ctypes.c_void_p * len(ts))(*(None if t is None else t.data_ptr() for t in ts))  # noqa
-            self.finalize_args = (E + 1, ptrs(self.work), self.info, ptrs([self.gbeta[i] for i in range(E)] + [None]),
+            self.finalize_args = (E + 1, ptrs(self.work), self.size_array(w.numel() * 4 for w in self.work), self.info,
+                                  ptrs([self.gbeta[i] for i in range(E)] + [None]),
                                   ptrs([self.galpha[i + 1] for i in range(E - 1)] + [None, self.galpha[0]]),
                                   self.K, self.C, 1, self.stream)
         return self.L.sihc_event_finalize(*self.finalize_args)
-
-    def _finalize_slots(self, slots, stream):
-        """sihc_event_finalize of the listed deferred slots of the one-stream step."""
-        E = self.E
-        key = ("one",) + tuple(slots)
-        if not hasattr(self, "fin_args"):
-            self.fin_args = {}
-        if key not in self.fin_args:
-            gb = [self.gbeta[i] for i in range(E)] + [None]
-            ga = [self.galpha[i + 1] for i in range(E - 1)] + [None, self.galpha[0]]
-            ptrs = lambda ts: (ctypes.c_void_p * len(ts))(*(None if t is None else t.data_ptr() for t in ts))  # noqa
-            info = (ctypes.c_int * (2 * len(slots)))()
-            self.fin_args[key] = (info, (len(slots), ptrs([self.work[k] for k in slots]), info,
-                                         ptrs([gb[k] for k in slots]), ptrs([ga[k] for k in slots]), self.K, self.C, 1))
-        info, args = self.fin_args[key]
-        for j, k in enumerate(slots):
-            info[2 * j], info[2 * j + 1] = self.info[2 * k], self.info[2 * k + 1]
-        self.check(self.L.sihc_event_finalize(*args, ctypes.c_void_p(stream.cuda_stream)))
-
-    def step_overlap(self):
-        """The one-stream step with the deferred finalize of the events already passed at
-        the middle of the backward run on a second stream, overlapping the rest of the
-        backward (the remaining events are finalized at the end, as in step())."""
-        torch = self.torch
-        main = torch.cuda.current_stream()
-        if not hasattr(self, "fin_stream1"):
-            self.fin_stream1 = torch.cuda.Stream(self.x[0].device)
-        E = self.E
-        mid_slot = E // 2
-        self.run(self.fwd)
-        body = self.bwd[:-1]  # without the deferred finalize of every event
-        mid_pos = E - 1 - mid_slot  # position of slot mid_slot's call in the backward list
-        for pos, (_, fn, args, _) in enumerate(body):
-            self.check(fn(*args))
-            if pos == mid_pos:
-                self.fin_stream1.wait_stream(main)
-                self._finalize_slots(list(range(mid_slot, E)), self.fin_stream1)
-        self._finalize_slots(list(range(mid_slot)) + [E], main)
-        main.wait_stream(self.fin_stream1)
 
     def run(self, calls):
         for _, fn, args, _ in calls:
@@ -1002,50 +965,37 @@ def main():
     print(f"[bench] building step: batch={args.batch} C={args.channels} events={args.events}", file=sys.stderr,
           flush=True)
     step = LiteralStep(args.batch, args.channels, args.events, args.seed)
-    overlap = args.finalize == "overlap"
     step.use_chain(args.finalize == "chain")
-    run_step = step.step_overlap if overlap else step.step
+    run_step = step.step
     torch.cuda.synchronize()
     for _ in range(args.warmup):
         run_step()
     torch.cuda.synchronize()
     print(f"[bench] warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
 
-    # Timed region: the K steps back to back, bracketed by device synchronisation. Inside
-    # each step HIP events mark only the step's phase boundaries and the two runs of full
-    # per-event launches (for the dominant kernels' average launch time). Steps with a
-    # second stream overlap launches, so those marks come from one-stream steps run after
-    # the timed region.
+    # Timed region: the K steps back to back, bracketed by device synchronisation, with no
+    # HIP event inside (an event record between two launches idles the GPU for several
+    # microseconds). The dominant kernels' average launch times and the phase split come
+    # from marked one-stream steps run after it: HIP events there mark only the phase
+    # boundaries and the two runs of full per-event launches.
     marks: list = []
-    t_fwd: list = []
     ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        a, c = ev(), ev()
-        a.record()
-        if overlap:
-            step.step_overlap()
-        else:
-            step.step(marks)
-        c.record()
-        t_fwd.append((a, c))
+        run_step()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = wall / args.steps * 1e3
-    step_ms = statistics.median(a.elapsed_time(c) for a, c in t_fwd)
-    one_stream_ms = None
-    if overlap:
-        t_one = []
-        for _ in range(max(2, min(args.steps, 5))):
-            a, c = ev(), ev()
-            a.record()
-            step.step(marks)
-            c.record()
-            t_one.append((a, c))
-        torch.cuda.synchronize()
-        one_stream_ms = statistics.median(a.elapsed_time(c) for a, c in t_one)
-        t_fwd = t_one
+    t_fwd = []
+    for _ in range(max(2, min(args.steps, 5))):
+        a, c = ev(), ev()
+        a.record()
+        step.step(marks)
+        c.record()
+        t_fwd.append((a, c))
+    torch.cuda.synchronize()
+    marked_ms = statistics.median(a.elapsed_time(c) for a, c in t_fwd)
     fwd_kern_ms = [f0.elapsed_time(f1) / nf for f0, f1, _, _, _, nf, _ in marks]
     kern_ms = [b0.elapsed_time(b1) / nb for _, _, _, b0, b1, _, nb in marks]
     avg_kernel_ms = statistics.median(kern_ms)
@@ -1083,8 +1033,7 @@ def main():
             "parallelism": "single GPU",
             "finalize": {"chain": "each backward launch finalizes the previous event's weight gradients in its "
                                   "trailing blocks (sihc_event_backward_chain)",
-                         "deferred": "one deferred finalize launch per 32 events after the last event",
-                         "overlap": "deferred finalize, half of it on a second stream"}[args.finalize],
+                         "deferred": "one deferred finalize launch per 32 events after the last event"}[args.finalize],
         },
         "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
         "tokens_per_s": round(args.batch * 256 / (ms_step * 1e-3), 1),
@@ -1092,7 +1041,7 @@ def main():
         "fwd_kernel_avg_ms": round(avg_fwd_kernel_ms, 4),
         "fwd_ms": round(fwd_ms, 3),
         "bwd_ms": round(bwd_ms, 3),
-        "one_stream_step_ms": None if one_stream_ms is None else round(one_stream_ms, 3),
+        "marked_step_ms": round(marked_ms, 3),
         "algorithmic_bytes_per_step": total_bytes,
         "roofline": {
             "kernel": ("k_event_bwd (sihc_event_backward_chain, full event, with the previous event's "

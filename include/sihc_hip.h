@@ -167,8 +167,9 @@ int sihc_event_backward_partial(const void *grad_x_out, const void *grad_z_out,
  * finalize of ONE earlier sihc_event_backward_partial / _chain call in its trailing
  * blocks: they are dispatched after every block of this event's backward and run while
  * its last round of blocks drains, so a chain of events needs no finalize launch except
- * for its last event. prev_workspace / prev_info / prev_grad_beta / prev_grad_alpha_next
- * are that call's workspace, info and gradients (a gradient its info does not list may be
+ * for its last event. prev_workspace / prev_workspace_bytes / prev_info / prev_grad_beta /
+ * prev_grad_alpha_next are that call's workspace (and its size: it must hold the partial
+ * rows prev_info lists), info and gradients (a gradient its info does not list may be
  * NULL); it must have used the same cell, channels and dtype, and its launch must precede
  * this one on `stream` (or have completed). prev_workspace must not overlap `workspace`,
  * nor its gradients this call's gradients or workspace (checked: SIHC_ERR_INVALID); two
@@ -182,15 +183,19 @@ int sihc_event_backward_chain(const void *grad_x_out, const void *grad_z_out,
                               void *grad_beta, void *grad_alpha_next, int64_t batch, int grid,
                               int cell, int channels, const int32_t *index, int dtype,
                               int w_dtype, void *workspace, size_t workspace_bytes, int *info,
-                              const void *prev_workspace, const int *prev_info,
-                              void *prev_grad_beta, void *prev_grad_alpha_next, void *stream);
+                              const void *prev_workspace, size_t prev_workspace_bytes,
+                              const int *prev_info, void *prev_grad_beta,
+                              void *prev_grad_alpha_next, void *stream);
 /* The deferred finalizes of n sihc_event_backward_partial calls (host arrays of n
- * workspaces, 2n info ints and n gradient pointers each, as passed to those calls; a
- * gradient the info does not list may be NULL): the fixed-order partial sums of each
- * event, stored in w_dtype. One launch per 32 events. */
-int sihc_event_finalize(int n, const void *const *workspaces, const int *info,
-                        void *const *grad_beta, void *const *grad_alpha_next, int cell,
-                        int channels, int w_dtype, void *stream);
+ * workspaces, their n sizes in bytes, 2n info ints and n gradient pointers each, as passed
+ * to those calls; a gradient the info does not list may be NULL): the fixed-order partial
+ * sums of each event, stored in w_dtype. One launch per 32 events. cell, channels and
+ * w_dtype must be those of the calls; a workspace smaller than the partial rows its info
+ * lists (info[2i] x 2 x cell^2 x channels x 4 bytes) is rejected with SIHC_ERR_INVALID
+ * before any launch. */
+int sihc_event_finalize(int n, const void *const *workspaces, const size_t *workspace_bytes,
+                        const int *info, void *const *grad_beta, void *const *grad_alpha_next,
+                        int cell, int channels, int w_dtype, void *stream);
 
 /* sihc_event_backward without a workspace argument, for callers that cannot allocate
  * device memory (code under HIP-graph capture, tight serving loops, harnesses that forbid
@@ -224,7 +229,10 @@ int sihc_scatter_cells(const void *cells, const int32_t *index, void *x, int64_t
  * allowed: x[pixel of (n, s)] = sum over the tokens t of batch b with index[b,t] == n, in
  * ascending t, of cells[b,t,s] (fp32 sum rounded once); cells no token selects are zero.
  * Atomics-free and deterministic; for a permutation index it equals sihc_scatter_cells
- * bit for bit. Out-of-range index values select no cell. index == NULL: the identity.
+ * bit for bit. Out-of-range index values (possible only when the caller skips validation)
+ * are clamped to the last cell, as sihc_gather_cells clamps them. index == NULL: the
+ * identity. Each output cell scans its batch row's grid*grid indices: O((grid*grid)^2)
+ * per batch row, grid*grid <= 16384.
  * No reference counterpart (the backward of the spatially indexed gather). */
 int sihc_scatter_add_cells(const void *cells, const int32_t *index, void *x, int64_t batch,
                            int grid, int cell, int channels, int dtype, void *stream);
@@ -238,6 +246,8 @@ int sihc_scatter_add_cells(const void *cells, const int32_t *index, void *x, int
  *          {carrier, workspace}, carriers 4 x `bytes` (1:1, 10 units);
  * shape 2: the per-event backward's arrays -- sources {carrier, carrier, workspace,
  *          workspace}, destinations {carrier, workspace} (2:1, 15 units).
+ * The library cannot see array sizes: with shapes 1 and 2 the carrier-shaped arrays MUST
+ * hold 4 x `bytes` bytes, or the kernel reads and writes past their ends.
  * No reference counterpart: the HBM ceiling the per-event kernels are read against. */
 int sihc_stream(const void *const *src, int nsrc, void *const *dst, int ndst, size_t bytes,
                 int shape, void *stream);

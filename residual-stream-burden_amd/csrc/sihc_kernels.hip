@@ -2534,7 +2534,11 @@ __global__ void __launch_bounds__(256) k_cells(const R* __restrict__ src, R* __r
 // cell: the batch row of the index is staged in LDS and every thread scans it in order
 // (a block-uniform test, so no divergence). No atomics: deterministic. The sum starts
 // from -0.0 (the identity of fp32 addition), so a cell with one contributor receives its
-// value bit for bit, as the scatter copy would.
+// value bit for bit, as the scatter copy would. Out-of-range indices (only possible when
+// the host-side validation is skipped) are clamped as the gather clamps them (to the last
+// cell), so the adjoint returns every gathered row's gradient to the cell it was read
+// from. Each block scans its batch row's GG indices per output vector: O(GG^2) work per
+// batch row, negligible at the benchmark grid (GG = 256) and bounded by GG <= 16384.
 // ----------------------------------------------------------------------------------
 template <typename T, int V, int K>
 __global__ void __launch_bounds__(256) k_cells_add(const T* __restrict__ cells, T* __restrict__ x,
@@ -2543,7 +2547,8 @@ __global__ void __launch_bounds__(256) k_cells_add(const T* __restrict__ cells, 
   extern __shared__ int32_t sidx[];
   const int64_t m = blockIdx.x;  // destination cell b * GG + n
   const int b = int(m / g.GG), n = int(m - int64_t(b) * g.GG);
-  for (int t = threadIdx.x; t < g.GG; t += blockDim.x) sidx[t] = index[int64_t(b) * g.GG + t];
+  for (int t = threadIdx.x; t < g.GG; t += blockDim.x)
+    sidx[t] = int32_t(min(uint32_t(index[int64_t(b) * g.GG + t]), uint32_t(g.GG) - 1u));
   __syncthreads();
   const int64_t pix0 = cell_pixel0(int(m), g, nullptr);
   const int nvec = S * g.C / V;
@@ -3810,8 +3815,9 @@ int sihc_event_backward_chain(const void* grad_x_out, const void* grad_z_out, co
                               const void* beta, const void* alpha_next, void* grad_x, void* grad_dz, void* grad_beta,
                               void* grad_alpha_next, int64_t batch, int grid, int cell, int channels,
                               const int32_t* index, int dtype, int w_dtype, void* workspace, size_t workspace_bytes,
-                              int* info, const void* prev_workspace, const int* prev_info, void* prev_grad_beta,
-                              void* prev_grad_alpha_next, void* stream) {
+                              int* info, const void* prev_workspace, size_t prev_workspace_bytes,
+                              const int* prev_info, void* prev_grad_beta, void* prev_grad_alpha_next,
+                              void* stream) {
   const char* what = "sihc_event_backward_chain";
   if (!info) return fail(SIHC_ERR_INVALID, "%s: null info", what);
   if (!prev_workspace)  // nothing carried: sihc_event_backward_partial
@@ -3830,6 +3836,9 @@ int sihc_event_backward_chain(const void* grad_x_out, const void* grad_z_out, co
   if (chunks > 0 && rows > 0) {
     if (((rows & 1) && !prev_grad_beta) || ((rows & 2) && !prev_grad_alpha_next))
       return fail(SIHC_ERR_INVALID, "%s: null gradient of the carried call", what);
+    if (prev_workspace_bytes < prev_bytes)
+      return fail(SIHC_ERR_INVALID, "%s: prev_workspace holds %zu bytes, its %d partial rows need %zu", what,
+                  prev_workspace_bytes, chunks, prev_bytes);
     if (!aligned(prev_workspace, 16)) return fail(SIHC_ERR_INVALID, "%s: prev_workspace must be 16-byte aligned", what);
     // the trailing blocks read prev_workspace and write the carried gradients while the
     // backward proper writes its own partial rows and gradients
@@ -3855,14 +3864,16 @@ int sihc_event_backward_chain(const void* grad_x_out, const void* grad_z_out, co
                              workspace_bytes, stream, info, cy.part ? &cy : nullptr);
 }
 
-int sihc_event_finalize(int n, const void* const* workspaces, const int* info, void* const* grad_beta,
-                        void* const* grad_alpha_next, int cell, int channels, int w_dtype, void* stream) {
+int sihc_event_finalize(int n, const void* const* workspaces, const size_t* workspace_bytes, const int* info,
+                        void* const* grad_beta, void* const* grad_alpha_next, int cell, int channels, int w_dtype,
+                        void* stream) {
   const char* what = "sihc_event_finalize";
   if (n < 0 || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
   if (cell != 2 && cell != 4) return fail(SIHC_ERR_INVALID, "%s: cell must be 2 or 4 (4 or 16 slots)", what);
   if (!valid_dtype(w_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype %d", what, w_dtype);
   if (n == 0) return SIHC_OK;
-  if (!workspaces || !info || !grad_beta || !grad_alpha_next) return fail(SIHC_ERR_INVALID, "%s: null array", what);
+  if (!workspaces || !workspace_bytes || !info || !grad_beta || !grad_alpha_next)
+    return fail(SIHC_ERR_INVALID, "%s: null array", what);
   const int S = cell * cell;
   // validate everything before the first launch
   for (int i = 0; i < n; ++i) {
@@ -3870,6 +3881,11 @@ int sihc_event_finalize(int n, const void* const* workspaces, const int* info, v
     if (chunks < 0 || rows < 0 || rows > 3) return fail(SIHC_ERR_INVALID, "%s: bad info of event %d", what, i);
     if (chunks == 0 || rows == 0) continue;
     if (!workspaces[i]) return fail(SIHC_ERR_INVALID, "%s: null workspace of event %d", what, i);
+    const size_t need = size_t(chunks) * 2 * S * size_t(channels) * sizeof(float);
+    if (workspace_bytes[i] < need)
+      return fail(SIHC_ERR_INVALID, "%s: workspace of event %d holds %zu bytes, its %d partial rows need %zu", what,
+                  i, workspace_bytes[i], chunks, need);
+    if (!aligned(workspaces[i], 16)) return fail(SIHC_ERR_INVALID, "%s: workspace of event %d misaligned", what, i);
     if (((rows & 1) && !grad_beta[i]) || ((rows & 2) && !grad_alpha_next[i]))
       return fail(SIHC_ERR_INVALID, "%s: null gradient of event %d", what, i);
   }

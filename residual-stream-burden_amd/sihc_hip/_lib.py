@@ -43,9 +43,10 @@ PROTOTYPES: dict[str, tuple] = {
                                            ctypes.POINTER(ctypes.c_int), _vp]),
     "sihc_event_backward_chain": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                          _i64, _i32, _i32, _i32, _vp, _i32, _i32, _vp, _sz,
-                                         ctypes.POINTER(ctypes.c_int), _vp, ctypes.POINTER(ctypes.c_int),
+                                         ctypes.POINTER(ctypes.c_int), _vp, _sz, ctypes.POINTER(ctypes.c_int),
                                          _vp, _vp, _vp]),
-    "sihc_event_finalize": (_i32, [_i32, _vpp, ctypes.POINTER(ctypes.c_int), _vpp, _vpp, _i32, _i32, _i32, _vp]),
+    "sihc_event_finalize": (_i32, [_i32, _vpp, ctypes.POINTER(_sz), ctypes.POINTER(ctypes.c_int), _vpp, _vpp,
+                                   _i32, _i32, _i32, _vp]),
     "sihc_event_backward_noalloc": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                            _i64, _i32, _i32, _i32, _vp, _i32, _i32, _vp]),
     "sihc_gather_cells": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
@@ -90,6 +91,11 @@ def check(rc: int) -> None:
     if rc != 0:
         msg = lib().sihc_last_error().decode(errors="replace")
         raise SihcError(msg or f"sihc call failed with code {rc}")
+
+
+def size_array(sizes) -> ctypes.Array:
+    sizes = list(sizes)
+    return (ctypes.c_size_t * max(1, len(sizes)))(*sizes)
 
 
 def ptr_array(ptrs) -> ctypes.Array:

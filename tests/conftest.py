@@ -43,9 +43,14 @@ def pytest_terminal_summary(terminalreporter):
         return
     tr = terminalreporter
     tr.section("parity margins")
-    for kind in ("elementwise", "reduced", "chained", "fp32"):
+    for kind in ("elementwise", "reduced", "chained", "fp32", "reference"):
         rows = [r for r in RECORDS if r[3] == kind]
         if not rows:
+            continue
+        if kind == "reference":  # r[5] holds the worst fraction of the reference's own bar
+            worst = max(rows, key=lambda r: r[5])
+            tr.write_line(f"{kind:11s} {len(rows):4d} checks; worst {worst[5]:.3f} of the reference's bar "
+                          f"({worst[1]}, {worst[0]})")
             continue
         worst_rel = max(rows, key=lambda r: r[7])
         line = f"{kind:11s} {len(rows):4d} checks; worst rel-L2 {worst_rel[7]:.2e} ({worst_rel[1]}, {worst_rel[0]})"

@@ -84,6 +84,26 @@ def assert_parity(actual: torch.Tensor, expected: torch.Tensor, dtype: torch.dty
         assert err <= 2e-2 * max(1.0, scale), f"{what}: bf16 max-abs {err:.3e} > 2e-2 * max(1, {scale:.3e})"
 
 
+def assert_close_reference(actual: torch.Tensor, expected: torch.Tensor, *, atol: float, rtol: float,
+                           what: str = "") -> None:
+    """The reference's own bar (torch.testing.assert_close semantics: |a - e| <= atol +
+    rtol * |e| for every element), for checks that mirror one of its tests with its
+    tolerances. Prints and records the achieved margin: the worst |a - e| / (atol + rtol*|e|)
+    (<= 1 passes) and the relative L2 error."""
+    a = actual.detach().double().cpu()
+    e = expected.detach().double().cpu()
+    assert a.shape == e.shape, f"{what}: shape {tuple(a.shape)} != {tuple(e.shape)}"
+    assert torch.isfinite(a).all(), f"{what}: non-finite values"
+    ratio = float(((a - e).abs() / (atol + rtol * e.abs())).max()) if e.numel() else 0.0
+    err = float((a - e).abs().max()) if e.numel() else 0.0
+    r = rel_l2(a, e) if e.numel() and float(e.norm()) > 0 else err
+    test = os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0]
+    RECORDS.append((test, what, "ref", "reference", err, ratio, float("nan"), r))
+    print(f"[parity] {what}: reference bar (atol {atol:g}, rtol {rtol:g}) worst {ratio:.3f} of the bar, "
+          f"max-abs {err:.3e} rel-L2 {r:.3e}", flush=True)
+    assert ratio <= 1.0, f"{what}: {ratio:.3f} x the reference's bar (atol {atol:g}, rtol {rtol:g})"
+
+
 def announce(msg: str) -> None:
     """Name the case on stdout before a GPU step (survives a box that dies mid-step)."""
     print(f"[case] {msg}", flush=True)

@@ -134,15 +134,22 @@ def test_deferred_finalize_arguments_are_validated():
     rc = lib.sihc_event_backward_partial(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
                                          2, 16, 2, 64, None, 1, 1, FAKE, 1 << 30, None, None)
     assert rc == 1 and b"null info" in lib.sihc_last_error()
-    assert lib.sihc_event_finalize(1, one, info, nul, one, 2, 64, 1, None) == 1
+    big = _lib.size_array([1 << 30])
+    assert lib.sihc_event_finalize(1, one, big, info, nul, one, 2, 64, 1, None) == 1
     assert b"null gradient of event 0" in lib.sihc_last_error()
     bad = (ctypes.c_int * 2)(7, 4)
-    assert lib.sihc_event_finalize(1, one, bad, one, one, 2, 64, 1, None) == 1
+    assert lib.sihc_event_finalize(1, one, big, bad, one, one, 2, 64, 1, None) == 1
     assert b"bad info" in lib.sihc_last_error()
-    assert lib.sihc_event_finalize(1, one, info, one, one, 3, 64, 1, None) == 1
-    assert lib.sihc_event_finalize(0, None, None, None, None, 2, 64, 1, None) == 0  # nothing to do
+    assert lib.sihc_event_finalize(1, one, big, info, one, one, 3, 64, 1, None) == 1
+    # 7 partial rows of 2 x 4 slots x 64 channels need 14,336 bytes
+    small = _lib.size_array([7 * 2 * 4 * 64 * 4 - 4])
+    assert lib.sihc_event_finalize(1, one, small, info, one, one, 2, 64, 1, None) == 1
+    assert b"partial rows need 14336" in lib.sihc_last_error()
+    assert lib.sihc_event_finalize(1, one, None, info, one, one, 2, 64, 1, None) == 1
+    assert b"null array" in lib.sihc_last_error()
+    assert lib.sihc_event_finalize(0, None, None, None, None, None, 2, 64, 1, None) == 0  # nothing to do
     empty = (ctypes.c_int * 2)(0, 0)  # a zero-token event: no partial rows, nothing read
-    assert lib.sihc_event_finalize(1, nul, empty, nul, nul, 2, 64, 1, None) == 0
+    assert lib.sihc_event_finalize(1, nul, _lib.size_array([0]), empty, nul, nul, 2, 64, 1, None) == 0
 
 
 def test_stream_calibration_arguments_are_validated():

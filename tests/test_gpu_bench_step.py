@@ -1,14 +1,13 @@
-"""GPU: the benchmark's config-2 step under its three finalize schedules computes the same
+"""GPU: the benchmark's config-2 step under its two finalize schedules computes the same
 bits. The step strings the per-event backward launches of a 56-event literal chain (here
 fewer events and a smaller batch) through the C ABI; the schedules differ only in where
 each event's weight-gradient partial rows are summed:
 
 * deferred: sihc_event_backward_partial for every event, then sihc_event_finalize;
 * chain: sihc_event_backward_chain, each launch finalizing the previous event's rows in
-  its trailing blocks, and one finalize launch for the last call;
-* overlap: the deferred schedule with half of the finalize on a second stream.
+  its trailing blocks, and one finalize launch for the last call.
 
-The partial rows and the fixed-order sums are the same in all three, so every output
+The partial rows and the fixed-order sums are the same in both, so every output
 (carrier and workspace gradients, dbeta, dalpha) must be bit-identical, step after step.
 """
 from __future__ import annotations
@@ -63,7 +62,3 @@ def test_finalize_schedules_are_bit_identical(batch, events):
         _poison(step)
         step.step()
         _same(_snapshot(step), deferred, f"chain step {r}")
-    step.use_chain(False)
-    _poison(step)
-    step.step_overlap()
-    _same(_snapshot(step), deferred, "overlapped finalize")

@@ -12,7 +12,7 @@ import copy
 import pytest
 import torch
 
-from helpers import announce, assert_parity, rel_l2
+from helpers import announce, assert_close_reference, assert_parity, rel_l2
 from oracle import sihc_oracle as O
 from sihc_hip.e2e import SiHCDenoiser
 
@@ -79,6 +79,40 @@ def test_bf16_model_matches_oracle_routing():
     with torch.no_grad():
         out, expected = model(x.bfloat16(), t, y), ref(x.bfloat16(), t, y)
     assert_parity(out, expected, torch.bfloat16, what="bf16 output", kind="chained")
+
+
+AUTOCAST_CASES = [(s, d, p) for s in ("stage", "literal") for d, p in ((8, 4), (12, 8), (20, 4))]
+
+
+@pytest.mark.parametrize("schedule,depth,patch", AUTOCAST_CASES,
+                         ids=[f"{s}-d{d}-p{p}" for s, d, p in AUTOCAST_CASES])
+def test_bf16_autocast_training_step_matches_oracle_routing(schedule, depth, patch):
+    # The training path the reference runs (fp32 parameters under bf16 autocast,
+    # sihc/training/train.py:633-639), output and every parameter gradient against the same
+    # model routed by the oracle's PyTorch read/write, with the reference's tolerances for
+    # this comparison (research/tests/test_sublayer_kernels.py:247-266: output by
+    # assert_numerics, gradients atol 5e-4 / rtol 0.15). Depth 8, 12 and 20 (stages 8,
+    # 12 and 8 + 12) with 4- and 16-slot cells (patch 8 and 4).
+    announce(f"e2e bf16 autocast {schedule} depth={depth} patch={patch}: output and all gradients")
+    stages = {8: (8,), 12: (12,), 20: (8, 12)}[depth]
+    torch.manual_seed(19)
+    model = SiHCDenoiser(hidden=64, depth=depth, heads=4, patch=patch, stages=stages,
+                         schedule=schedule).random_init(seed=19).cuda()
+    ref = _oracle_routing(copy.deepcopy(model))
+    ref.event = lambda x, dz, beta, alpha: O.event_forward(x, dz, beta, alpha)
+    x, t, y = _inputs(batch=1, seed=7)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        out = model(x, t, y)
+        expected = ref(x, t, y)
+    assert out.dtype == torch.bfloat16
+    out.float().square().mean().backward()
+    expected.float().square().mean().backward()
+    assert_parity(out, expected, torch.bfloat16, what="autocast output", kind="chained")
+    assert_close_reference(out, expected, atol=0.025, rtol=0.03, what="autocast output")
+    for (name, a), (_, b) in zip(model.named_parameters(), ref.named_parameters()):
+        assert a.grad is not None and b.grad is not None, name
+        assert torch.isfinite(a.grad).all(), name
+        assert_close_reference(a.grad, b.grad, atol=5e-4, rtol=0.15, what=f"grad {name}")
 
 
 @pytest.mark.parametrize("schedule", ["stage", "literal"])

@@ -160,12 +160,14 @@ def _finalize_chain_case(dtype, slots, n, seed):
     return cases, c, k
 
 
-def _run_partial(L, entry, case, c, k, code, work, info_slot, prev, st):
+def _run_partial(L, entry, case, c, k, code, work, info_slot, prev, st, reuse=None):
     import ctypes
 
     p = lambda t: None if t is None or t.numel() == 0 else ctypes.c_void_p(t.data_ptr())  # noqa: E731
     mode, b, args, ref = case
     outs = [torch.full_like(t, float("nan")) if t is not None else None for t in ref]
+    if reuse is not None:  # this call's weight gradients in the given tensors
+        outs[2], outs[3] = reuse[2], reuse[3]
     gx = outs[0] if mode != "write" else torch.full_like(ref[0], float("nan"))
     hh, gz, xo, d, bt, al = args
     call = (p(hh), p(gz), p(xo), p(d), p(bt), p(al), p(gx), p(outs[1]), p(outs[2]), p(outs[3]), b, 16, k, c, None,
@@ -208,8 +210,8 @@ def test_deferred_finalize_matches_per_call_finalize(dtype, slots):
         got.append(_run_partial(L, "partial", case, c, k, code, works[-1], slot(i), None, st))
     assert info[2 * (n // 2)] == 0, "the call without tokens leaves no partial rows"
     vp = lambda ts: _lib.ptr_array(None if t is None else t.data_ptr() for t in ts)  # noqa: E731
-    _lib.check(L.sihc_event_finalize(n, vp(works), info, vp([o[2] for o in got]), vp([o[3] for o in got]),
-                                     k, c, code, st))
+    _lib.check(L.sihc_event_finalize(n, vp(works), _lib.size_array(w.numel() * 4 for w in works), info,
+                                     vp([o[2] for o in got]), vp([o[3] for o in got]), k, c, code, st))
     torch.cuda.synchronize()
     for i, (a, case) in enumerate(zip(got, cases)):
         for j in range(4):
@@ -242,10 +244,12 @@ def test_chained_finalize_matches_per_call_finalize(dtype, slots):
     got = []
     p = lambda t: None if t is None else ctypes.c_void_p(t.data_ptr())  # noqa: E731
     for i, case in enumerate(cases):
-        prev = (None, None, None, None) if i == 0 else \
-            (p(works[(i - 1) % 2]), slot(i - 1), p(got[-1][2]), p(got[-1][3]))
+        prev = (None, 0, None, None, None) if i == 0 else \
+            (p(works[(i - 1) % 2]), works[(i - 1) % 2].numel() * 4, slot(i - 1), p(got[-1][2]), p(got[-1][3]))
         got.append(_run_partial(L, "chain", case, c, k, code, works[i % 2], slot(i), prev, st))
-    _lib.check(L.sihc_event_finalize(1, _lib.ptr_array([works[(n - 1) % 2].data_ptr()]), slot(n - 1),
+    last = works[(n - 1) % 2]
+    _lib.check(L.sihc_event_finalize(1, _lib.ptr_array([last.data_ptr()]), _lib.size_array([last.numel() * 4]),
+                                     slot(n - 1),
                                      _lib.ptr_array([None if got[-1][2] is None else got[-1][2].data_ptr()]),
                                      _lib.ptr_array([None if got[-1][3] is None else got[-1][3].data_ptr()]),
                                      k, c, code, st))
@@ -274,5 +278,12 @@ def test_chained_finalize_rejects_overlapping_workspaces():
     p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     with pytest.raises(_lib.SihcError, match="overlaps this call's workspace"):
         _run_partial(L, "chain", cases[0], c, k, _lib.DTYPE_BF16, work, slot(1),
-                     (p(work), slot(0), p(got[2]), p(got[3])), st)
+                     (p(work), work.numel() * 4, slot(0), p(got[2]), p(got[3])), st)
+    other = torch.empty_like(work)
+    with pytest.raises(_lib.SihcError, match="partial rows need"):
+        _run_partial(L, "chain", cases[0], c, k, _lib.DTYPE_BF16, other, slot(1),
+                     (p(work), 4096, slot(0), p(got[2]), p(got[3])), st)
+    with pytest.raises(_lib.SihcError, match="overlap this call's"):
+        _run_partial(L, "chain", cases[0], c, k, _lib.DTYPE_BF16, other, slot(1),
+                     (p(work), work.numel() * 4, slot(0), p(got[2]), p(got[3])), st, reuse=got)
     torch.cuda.synchronize()

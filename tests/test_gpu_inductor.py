@@ -18,8 +18,9 @@ import time
 import pytest
 import torch
 
-from helpers import announce, assert_parity
+from helpers import announce, assert_close_reference, assert_parity
 from sihc_hip import sublayer_kernels
+from sihc_hip.sublayer_kernels import sublayer_triangular
 from sihc_hip.e2e import SiHCDenoiser
 
 pytestmark = pytest.mark.gpu
@@ -91,3 +92,46 @@ def test_inductor_fullgraph_forward_backward(schedule, depth, patch, bf16, tri, 
         assert torch.isfinite(g).all(), name
         torch.testing.assert_close(g, eager_grads[name], atol=5e-4 if bf16 else 3e-5,
                                    rtol=0.15 if bf16 else 0.003, msg=name)
+
+
+TRI_CASES = [(d, a, tri) for d in (torch.float32, torch.bfloat16) for a in (3, 23) for tri in ("visible", "fused")]
+
+
+@pytest.mark.parametrize("dtype,active,tri", TRI_CASES,
+                         ids=[f"{str(d)[6:]}-a{a}-{t}" for d, a, t in TRI_CASES])
+def test_triangular_compiled_gradient_accumulation_and_tails(dtype, active, tri, monkeypatch):
+    # The triangular op alone under torch.compile(mode="default", fullgraph=True), with the
+    # reference's case (research/tests/test_sublayer_kernels.py:185-213): 3 x 49 rows x 67
+    # channels (token and channel tails), an fp32 gamma with a bf16 (or fp32) workspace, and a
+    # second loss term on every update, so the compiled backward must add the triangular
+    # op's update gradient to the update's own gradient. Eager, compiled and a plain
+    # PyTorch restatement agree within the reference's tolerances; both traced forms of
+    # the op's backward are compiled.
+    announce(f"inductor triangular op dtype={dtype} active={active} traced backward={tri}")
+    monkeypatch.setattr(sublayer_kernels, "COMPILED_TRIANGULAR_BACKWARD", tri)
+    torch.manual_seed(583)
+    base = torch.randn(3, 49, 67, device="cuda", dtype=dtype).requires_grad_()
+    updates = [torch.randn_like(base).requires_grad_() for _ in range(active)]
+    gamma = (torch.randn(active, 67, device="cuda") * 0.05).requires_grad_()  # fp32 gamma
+    inputs = (base, *updates, gamma)
+
+    def fn(base, updates, gamma):
+        out = sublayer_triangular(base, updates, gamma)
+        return out.float().square().mean() + sum(u.float().square().mean() for u in updates)
+
+    loss = fn(base, updates, gamma)
+    eager = torch.autograd.grad(loss, inputs)
+    ref = (base.float() + sum(u.float() * g for u, g in zip(updates, gamma))).to(dtype)
+    ref_loss = ref.float().square().mean() + sum(u.float().square().mean() for u in updates)
+    expected = torch.autograd.grad(ref_loss, inputs)
+    compiled = torch.compile(fn, mode="default", fullgraph=True)
+    actual = compiled(base, updates, gamma)
+    compiled_grads = torch.autograd.grad(actual, inputs)
+    tol = dict(atol=2e-4, rtol=2e-4) if dtype == torch.float32 else dict(atol=0.025, rtol=0.03)
+    assert_close_reference(actual, loss, what="compiled loss", **tol)
+    names = ["base"] + [f"update {j}" for j in range(active)] + ["gamma"]
+    gtol = dict(atol=1e-7, rtol=3e-4) if dtype == torch.float32 else dict(atol=2e-5, rtol=0.035)
+    for name, a, b, c in zip(names, eager, expected, compiled_grads):
+        assert a.dtype == b.dtype == c.dtype, name
+        assert_close_reference(a, b, what=f"eager grad {name} vs plain PyTorch", **gtol)
+        assert_close_reference(c, a, what=f"compiled grad {name} vs eager", **gtol)
