@@ -595,8 +595,11 @@ def traffic_from_profiles() -> float | None:
 
 def calibrate(args) -> None:
     """Launches for rocprofv3 counter runs: the library's copy kernel over a known byte
-    count (the FETCH_SIZE/WRITE_SIZE scale), then one per-event forward and one full
-    per-event backward at the benchmark shape, 3 times each."""
+    count (the FETCH_SIZE/WRITE_SIZE scale), 3 per-event forwards, then 4 full per-event
+    backwards at the benchmark shape as the step launches them: a first
+    sihc_event_backward_partial, then 3 sihc_event_backward_chain calls, each finalizing the
+    previous call's partial rows in its trailing blocks (the dispatches 2-4 are the ones the
+    step repeats 54 times)."""
     import torch
 
     step = LiteralStep(args.batch, args.channels, 2, args.seed)
@@ -613,19 +616,31 @@ def calibrate(args) -> None:
     vp = ctypes.c_void_p
     p = lambda t: vp(t.data_ptr())  # noqa: E731
     B, G, K, C = step.B, step.G, step.K, step.C
-    bwd_args = (p(step.h_out), p(step.gz[1]), p(step.x[1]), p(step.dz[0]), p(step.beta[0]), p(step.alpha[1]),
-                p(step.gx[0]), p(step.gdz[0]), p(step.gbeta[0]), p(step.galpha[1]), B, G, K, C, None, 1, 1,
-                p(step.work[0]), step.work[0].numel() * 4, step.stream)
+    nwork = step.work[0].numel() * 4
+    info = (ctypes.c_int * 8)()
+    slot = lambda k: ctypes.cast(ctypes.addressof(info) + 8 * k, ctypes.POINTER(ctypes.c_int))  # noqa: E731
+    grads = [(torch.empty_like(step.gbeta[0]), torch.empty_like(step.galpha[1])) for _ in range(4)]
+    works = [step.work[0], step.work[1]]
+
+    def bwd_args(k):
+        return (p(step.h_out), p(step.gz[1]), p(step.x[1]), p(step.dz[0]), p(step.beta[0]), p(step.alpha[1]),
+                p(step.gx[0]), p(step.gdz[0]), p(grads[k][0]), p(grads[k][1]), B, G, K, C, None, 1, 1,
+                p(works[k % 2]), nwork, slot(k))
+
     for _ in range(3):
         check(fwd[1](*fwd[2]))
-    for _ in range(3):
-        check(L.sihc_event_backward(*bwd_args))
+    check(L.sihc_event_backward_partial(*bwd_args(0), step.stream))
+    for k in range(1, 4):
+        prev = (p(works[(k - 1) % 2]), nwork, slot(k - 1), p(grads[k - 1][0]), p(grads[k - 1][1]))
+        check(L.sihc_event_backward_chain(*bwd_args(k), *prev, step.stream))
     torch.cuda.synchronize()
     U = step.M * C * ELEM
+    rows = info[6] * 2 * step.S * C * 4  # partial rows of one launch
     print(json.dumps({"copy_bytes_read": copy_bytes, "copy_bytes_written": copy_bytes,
                       "event_forward_bytes": fwd[3], "event_backward_bytes": 15 * U + 4 * C * 4 * ELEM,
                       "event_forward_read": 5 * U, "event_forward_written": 5 * U,
-                      "event_backward_read": 10 * U, "event_backward_written": 5 * U}), flush=True)
+                      "event_backward_read": 10 * U, "event_backward_written": 5 * U,
+                      "event_backward_partial_rows_bytes": rows}), flush=True)
 
 
 def kernels(args) -> None:
