@@ -410,25 +410,45 @@ def extra_configs(seed: int) -> dict:
     }
     del xs, dz, x0
     torch.cuda.empty_cache()
-    # ---- config 3
+    # ---- config 3: preallocated buffers, launches through the C ABI (as the config-2 step),
+    # the backward with its own finalize launch (sihc_event_backward)
+    from sihc_hip import _lib
+
+    L3 = _lib.lib()
+    st3 = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    vp = ctypes.c_void_p
     B, C, S = 128, 1152, 4
     U = B * 256 * C * ELEM
     x = r((B, 32, 32, C))
     idx = group_index(B, 16, 5, seed=3).to(dev)
     d = r((B, 256, C))
     bw, aw = r((C, S), 1.0, 0.02), r((C, S), 0.25, 0.02)
-    xo, zo = launch.event_forward(x, d, bw, aw, index=idx)
     h, gz = r((B, 32, 32, C), 0.0, 1e-2), r((B, 256, C), 0.0, 1e-2)
+    xo, zo, gx3 = torch.empty_like(x), torch.empty_like(d), torch.empty_like(x)
+    gdz3, gb3, ga3 = torch.empty_like(d), torch.empty_like(bw), torch.empty_like(aw)
+    nws3 = L3.sihc_event_backward_workspace_size(B, 16, 2, C)
+    ws3 = torch.empty(nws3, dtype=torch.uint8, device=dev)
+    p3 = lambda t: vp(t.data_ptr())  # noqa: E731
+
+    def fwd3(ix):
+        _lib.check(L3.sihc_event_forward(p3(x), p3(d), p3(bw), p3(aw), p3(xo), p3(zo), B, 16, 2, C,
+                                         None if ix is None else p3(ix), 1, st3))
+
+    def bwd3(ix):
+        _lib.check(L3.sihc_event_backward(p3(h), p3(gz), p3(xo), p3(d), p3(bw), p3(aw), p3(gx3), p3(gdz3),
+                                          p3(gb3), p3(ga3), B, 16, 2, C, None if ix is None else p3(ix), 1, 1,
+                                          p3(ws3), nws3, st3))
+
+    fwd3(idx)
     cells = launch.gather_cells(x, idx, S)
-    t_f = _timed(torch, lambda: launch.event_forward(x, d, bw, aw, index=idx))
-    t_b = _timed(torch, lambda: launch.event_backward(h, gz, xo, d, bw, aw, index=idx))
+    t_f, t_b = _timed(torch, lambda: fwd3(idx), iters=20), _timed(torch, lambda: bwd3(idx), iters=20)
     t_g = _timed(torch, lambda: launch.gather_cells(x, idx, S))
     t_s = _timed(torch, lambda: launch.scatter_cells(cells, idx))
-    # the same calls without the index, for the cost of the index at this batch
-    t_fu = _timed(torch, lambda: launch.event_forward(x, d, bw, aw))
-    t_bu = _timed(torch, lambda: launch.event_backward(h, gz, xo, d, bw, aw))
+    # the same launches without the index, for the cost of the index at this batch
+    t_fu, t_bu = _timed(torch, lambda: fwd3(None), iters=20), _timed(torch, lambda: bwd3(None), iters=20)
     out["config3_indexed"] = {
-        "workload": "batch 128, D=1152, int32 state index (seeded groups of 5), bf16",
+        "workload": "batch 128, D=1152, int32 state index (seeded groups of 5), bf16; C-ABI launches on "
+                    "preallocated buffers, backward with its finalize launch",
         "event_forward_GB/s": round(10 * U / t_f / 1e9, 1), "event_backward_GB/s": round(15 * U / t_b / 1e9, 1),
         "unindexed_event_forward_GB/s": round(10 * U / t_fu / 1e9, 1),
         "unindexed_event_backward_GB/s": round(15 * U / t_bu / 1e9, 1),
