@@ -1861,8 +1861,13 @@ __global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgradz_d2(const bf16_t*
 // bits, do not depend on NV.
 // ----------------------------------------------------------------------------------
 // Block of 256 threads (`tid` = flat thread index); `red` holds FINALIZE_LDS floats of LDS.
+#ifndef FINALIZE_FO
 #define FINALIZE_FO 32  // output lanes of a block (each NV outputs)
-#define FINALIZE_FG 8   // chunk groups of a block
+#endif
+#ifndef FINALIZE_FG
+#define FINALIZE_FG 8   // chunk groups of a block (FINALIZE_FO x FINALIZE_FG = 256 threads)
+#endif
+static_assert(FINALIZE_FO * FINALIZE_FG == 256, "finalize blocks are 256 threads");
 #define FINALIZE_LDS(NV) (FINALIZE_FG * FINALIZE_FO * (NV))
 template <typename TO, int NV>
 __device__ __forceinline__ void finalize_outputs(const float* __restrict__ part, TO* __restrict__ out0,
@@ -2943,7 +2948,7 @@ int launch_finalize(const char* what, const float* part, void* out0, void* out1,
   const bool wide = (int64_t(S) * C) % 4 == 0 && aligned(part, 16);
   auto go = [&](auto nv) {
     constexpr int NV = decltype(nv)::value;
-    const unsigned blocks = unsigned((n + 32 * NV - 1) / (32 * NV));
+    const unsigned blocks = unsigned((n + FINALIZE_FO * NV - 1) / (FINALIZE_FO * NV));
     if (out_dtype == SIHC_DTYPE_F32) {
       hipLaunchKernelGGL((k_finalize<float, NV>), dim3(blocks), dim3(256), 0, st, part, static_cast<float*>(out0),
                          static_cast<float*>(out1), chunks, R, S, C, pair ? 1 : 0, zero_mask);
@@ -3890,7 +3895,8 @@ int sihc_event_finalize(int n, const void* const* workspaces, const size_t* work
       return fail(SIHC_ERR_INVALID, "%s: null gradient of event %d", what, i);
   }
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const unsigned bx = unsigned((int64_t(2) * S * channels + 127) / 128);  // 128 outputs per block
+  const unsigned bx = unsigned((int64_t(2) * S * channels + EV_CARRY_OUTPUTS_PER_BLOCK - 1) /
+                               EV_CARRY_OUTPUTS_PER_BLOCK);  // FINALIZE_FO x 4 outputs per block
   for (int i0 = 0; i0 < n; i0 += SIHC_FINALIZE_BATCH) {
     FinalizeBatch b{};
     int nb = 0;
