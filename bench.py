@@ -416,6 +416,23 @@ def extra_configs(seed: int) -> dict:
     }
     del xs, dz, x0
     torch.cuda.empty_cache()
+    out["config3_indexed"] = config3_indexed(seed)
+    return out
+
+
+def config3_indexed(seed: int) -> dict:
+    """Benchmark config 3 (batch 128, D=1152, bf16, the seeded group-of-5 state index):
+    the per-event fused forward and backward through the index and without it, and the
+    explicit bit-exact gather/scatter of every token's state."""
+    import torch
+
+    from sihc_hip import launch
+    from sihc_hip.indexed import group_index
+
+    dev = torch.device("cuda", 0)
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(seed + 3)
+    r = lambda shape, m=0.0, sd=1.0: (m + sd * torch.randn(shape, device=dev, generator=g)).to(bf)  # noqa: E731
     # ---- config 3: preallocated buffers, launches through the C ABI (as the config-2 step),
     # the backward with its own finalize launch (sihc_event_backward)
     from sihc_hip import _lib
@@ -447,12 +464,17 @@ def extra_configs(seed: int) -> dict:
 
     fwd3(idx)
     cells = launch.gather_cells(x, idx, S)
+    # fresh buffers: the first few dozen launches over them run several % slower, so both
+    # the indexed and the unindexed launches warm up before either is timed
+    for _ in range(10):
+        fwd3(idx), bwd3(idx), fwd3(None), bwd3(None)
+    fwd3(idx)
     t_f, t_b = _timed(torch, lambda: fwd3(idx), iters=20), _timed(torch, lambda: bwd3(idx), iters=20)
     t_g = _timed(torch, lambda: launch.gather_cells(x, idx, S))
     t_s = _timed(torch, lambda: launch.scatter_cells(cells, idx))
     # the same launches without the index, for the cost of the index at this batch
     t_fu, t_bu = _timed(torch, lambda: fwd3(None), iters=20), _timed(torch, lambda: bwd3(None), iters=20)
-    out["config3_indexed"] = {
+    return {
         "workload": "batch 128, D=1152, int32 state index (seeded groups of 5), bf16; C-ABI launches on "
                     "preallocated buffers, backward with its finalize launch",
         "event_forward_GB/s": round(10 * U / t_f / 1e9, 1), "event_backward_GB/s": round(15 * U / t_b / 1e9, 1),
@@ -461,7 +483,6 @@ def extra_configs(seed: int) -> dict:
         "gather_GB/s": round(2 * S * U / t_g / 1e9, 1), "scatter_GB/s": round(2 * S * U / t_s / 1e9, 1),
         "event_fwd_bwd_tokens_per_s": round(B * 256 / (t_f + t_b), 1),
     }
-    return out
 
 
 def stage_api_config2(seed: int, steps: int = 3, compiled: bool = False) -> dict:
