@@ -4,7 +4,8 @@
  * Shows that the library needs nothing but the HIP runtime and this header: it
  * allocates device buffers, calls read / write / weight gradient / triangular /
  * fused triangular backward, the per-event fused forward and backward (with and
- * without a state index) and the cell gather / scatter on small fp32 shapes, and
+ * without a state index; also as a deferred call followed by a chained call that
+ * finalizes it) and the cell gather / scatter on small fp32 shapes, and
  * checks every result against direct loops over the cell index map (token
  * m = b*G*G + n reads cell n, or cell index[m] with a state index; cell n = wy*G + wx,
  * slot s = uy*K + ux -> carrier pixel (b, wy*K + uy, wx*K + ux)), plus one argument
@@ -274,6 +275,48 @@ int main(void) {
       check(name, gb, want_b, C * S, 1e-5);
       snprintf(name, sizeof name, "event backward dalpha'%s", use_idx ? " (index)" : "");
       check(name, ga, want_a, C * S, 1e-5);
+      /* the same backward twice as a chain: a deferred call (sihc_event_backward_partial),
+         then a chained call whose trailing blocks finalize the first call's partial rows,
+         then the finalize of the second call; every weight gradient bit-equal to
+         sihc_event_backward's */
+      {
+        static float gb1[C * S], ga1[C * S], gb2[C * S], ga2[C * S];
+        float *dgb1, *dga1, *dgb2, *dga2;
+        void *ework2;
+        int info1[2], info2[2];
+        HIP_OK(hipMalloc((void **)&dgb1, sizeof gb1));
+        HIP_OK(hipMalloc((void **)&dga1, sizeof ga1));
+        HIP_OK(hipMalloc((void **)&dgb2, sizeof gb2));
+        HIP_OK(hipMalloc((void **)&dga2, sizeof ga2));
+        HIP_OK(hipMalloc(&ework2, ebytes));
+        SIHC_OK_(sihc_event_backward_partial(dgxo, dgzo, dxo, dz[0], dbeta, dalpha + C * S, dgx, dgdz, dgb1, dga1,
+                                             B, G, K, C, use_idx ? didx : NULL, SIHC_DTYPE_F32, SIHC_DTYPE_F32,
+                                             ework, ebytes, info1, NULL));
+        SIHC_OK_(sihc_event_backward_chain(dgxo, dgzo, dxo, dz[0], dbeta, dalpha + C * S, dgx, dgdz, dgb2, dga2, B,
+                                           G, K, C, use_idx ? didx : NULL, SIHC_DTYPE_F32, SIHC_DTYPE_F32, ework2,
+                                           ebytes, info2, ework, ebytes, info1, dgb1, dga1, NULL));
+        const void *w2[1] = {ework2};
+        const size_t n2[1] = {ebytes};
+        void *gb2p[1] = {dgb2}, *ga2p[1] = {dga2};
+        SIHC_OK_(sihc_event_finalize(1, w2, n2, info2, gb2p, ga2p, K, C, SIHC_DTYPE_F32, NULL));
+        HIP_OK(hipMemcpy(gb1, dgb1, sizeof gb1, hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(ga1, dga1, sizeof ga1, hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(gb2, dgb2, sizeof gb2, hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(ga2, dga2, sizeof ga2, hipMemcpyDeviceToHost));
+        snprintf(name, sizeof name, "chain: carried dbeta%s", use_idx ? " (idx)" : "");
+        bit_equal(name, gb1, gb, C * S);
+        snprintf(name, sizeof name, "chain: carried dalpha'%s", use_idx ? " (idx)" : "");
+        bit_equal(name, ga1, ga, C * S);
+        snprintf(name, sizeof name, "chain: last dbeta%s", use_idx ? " (idx)" : "");
+        bit_equal(name, gb2, gb, C * S);
+        snprintf(name, sizeof name, "chain: last dalpha'%s", use_idx ? " (idx)" : "");
+        bit_equal(name, ga2, ga, C * S);
+        (void)hipFree(dgb1);
+        (void)hipFree(dga1);
+        (void)hipFree(dgb2);
+        (void)hipFree(dga2);
+        (void)hipFree(ework2);
+      }
     }
 
     /* gather / scatter of whole cells: bit-exact copies; scatter(gather(x)) == x */
