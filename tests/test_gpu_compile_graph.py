@@ -159,3 +159,75 @@ def test_hip_graph_capture_of_a_cold_weight_gradient():
         expected = launch.weight_grad(x, ups, w, out_dtype=torch.float32)
         torch.cuda.synchronize()
         assert torch.equal(static_out, expected), f"replay {r} differs from eager"
+
+
+def test_hip_graph_capture_of_a_chained_event_backward():
+    # Three per-event backwards as the benchmark step launches them -- a deferred call,
+    # two chained calls each finalizing its predecessor's partial rows in its trailing
+    # blocks, then the last call's finalize -- captured into one HIP graph (no memset is
+    # recorded: every partial row is written before it is read) and replayed with fresh
+    # inputs and eager work in between: every replay bit-equal to the eager chain.
+    import ctypes
+
+    from sihc_hip import _lib
+
+    announce("hip graph chained event backward")
+    torch.manual_seed(7)
+    L = _lib.lib()
+    b, c, n = 2, 72, 3
+    bf = torch.bfloat16
+    x_out = torch.randn(b, 32, 32, c, device="cuda").to(bf)
+    dz = [torch.randn(b, 256, c, device="cuda").to(bf) for _ in range(n)]
+    h = (1e-2 * torch.randn(b, 32, 32, c, device="cuda")).to(bf)
+    gz = (1e-2 * torch.randn(b, 256, c, device="cuda")).to(bf)
+    beta = [(1.0 + 0.05 * torch.randn(c, 4, device="cuda")).to(bf) for _ in range(n)]
+    alpha = [(0.25 + 0.05 * torch.randn(c, 4, device="cuda")).to(bf) for _ in range(n)]
+    nws = L.sihc_event_backward_workspace_size(b, 16, 2, c)
+    works = [torch.empty(nws // 4 + 16, device="cuda") for _ in range(2)]
+    info = (ctypes.c_int * (2 * n))()
+    slot = lambda i: ctypes.cast(ctypes.addressof(info) + 8 * i, ctypes.POINTER(ctypes.c_int))  # noqa: E731
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+
+    def outputs():
+        return ([torch.empty_like(x_out) for _ in range(n)], [torch.empty_like(dz[0]) for _ in range(n)],
+                [torch.empty_like(beta[0]) for _ in range(n)], [torch.empty_like(alpha[0]) for _ in range(n)])
+
+    def chain(out):
+        gx, gdz, gb, ga = out
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for i in range(n):
+            args = (p(h), p(gz), p(x_out), p(dz[i]), p(beta[i]), p(alpha[i]), p(gx[i]), p(gdz[i]), p(gb[i]),
+                    p(ga[i]), b, 16, 2, c, None, _lib.DTYPE_BF16, _lib.DTYPE_BF16, p(works[i % 2]),
+                    works[i % 2].numel() * 4, slot(i))
+            if i == 0:
+                _lib.check(L.sihc_event_backward_partial(*args, st))
+            else:
+                prev = works[(i - 1) % 2]
+                _lib.check(L.sihc_event_backward_chain(*args, p(prev), prev.numel() * 4, slot(i - 1), p(gb[i - 1]),
+                                                       p(ga[i - 1]), st))
+        last = works[(n - 1) % 2]
+        _lib.check(L.sihc_event_finalize(1, _lib.ptr_array([last.data_ptr()]), _lib.size_array([last.numel() * 4]),
+                                         slot(n - 1), _lib.ptr_array([gb[-1].data_ptr()]),
+                                         _lib.ptr_array([ga[-1].data_ptr()]), 2, c, _lib.DTYPE_BF16, st))
+
+    static = outputs()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        chain(static)  # warm-up: occupancy queries and info slots
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        chain(static)
+    for r in range(3):
+        with torch.no_grad():
+            h.copy_((1e-2 * torch.randn_like(h.float())).to(bf))
+            gz.copy_((1e-2 * torch.randn_like(gz.float())).to(bf))
+        graph.replay()
+        eager = outputs()
+        chain(eager)  # eager work between the replays
+        torch.cuda.synchronize()
+        for k, (a_list, e_list) in enumerate(zip(static, eager)):
+            for i, (a, e) in enumerate(zip(a_list, e_list)):
+                assert torch.equal(a, e), f"replay {r}: output {k} of event {i} differs from eager"
