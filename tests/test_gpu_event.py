@@ -34,6 +34,40 @@ def test_event_forward_matches_write_then_read(dtype, slots, channels):
     assert none is None and torch.equal(x_only, x_out)
 
 
+def _offset_copy(t: torch.Tensor) -> torch.Tensor:
+    """The same values, stored one element past a 16-byte boundary."""
+    buf = torch.empty(t.numel() + 1, device=t.device, dtype=t.dtype)
+    out = buf[1:].view(t.shape)
+    out.copy_(t)
+    return out
+
+
+@pytest.mark.parametrize("channels,batch,grid", [(8, 3, 7), (1152, 2, 9), (1160, 2, 5), (5776, 1, 3)])
+def test_event_forward_whole_row_blocks(channels, batch, grid):
+    # 4-slot bf16 cells with 16-byte aligned rows run on whole-row blocks of C/8 lanes and
+    # max(1, 720 // (C/8)) tokens: 1 lane x 720 tokens (C=8), 144 x 5 and 145 x 4 with a
+    # partial last block (162 and 50 tokens), 722 lanes x 1 token (C=5776). The same call
+    # on rows one element off a 16-byte boundary takes the general kernel: same bits.
+    announce(f"event fwd whole rows C={channels} batch={batch} grid={grid}")
+    torch.manual_seed(channels + grid)
+    dt = torch.bfloat16
+    x = torch.randn(batch, 2 * grid, 2 * grid, channels, device="cuda", dtype=dt)
+    dz = torch.randn(batch, grid * grid, channels, device="cuda", dtype=dt)
+    beta = (1.0 + 0.02 * torch.randn(channels, 4, device="cuda")).to(dt)
+    alpha = (0.25 + 0.02 * torch.randn(channels, 4, device="cuda")).to(dt)
+    x_out, z_out = launch.event_forward(x, dz, beta, alpha)
+    rx, rz = O.event_forward(x.cpu(), dz.cpu(), beta.cpu(), alpha.cpu())
+    assert_parity(x_out, rx, dt, what="x_out")
+    assert_parity(z_out, rz, dt, what="z_out")
+    xg, zg = launch.event_forward(_offset_copy(x), _offset_copy(dz), beta, alpha)
+    assert torch.equal(xg, x_out) and torch.equal(zg, z_out)
+    # a per-image permutation of the grid's cells: every carrier cell is written
+    idx = torch.stack([torch.randperm(grid * grid) for _ in range(batch)]).to(torch.int32).cuda()
+    xi, zi = launch.event_forward(x, dz, beta, alpha, index=idx)
+    xgi, zgi = launch.event_forward(_offset_copy(x), _offset_copy(dz), beta, alpha, index=idx)
+    assert torch.equal(xi, xgi) and torch.equal(zi, zgi)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("slots", [4, 16])
 @pytest.mark.parametrize("has_h,has_g", [(True, True), (False, True), (True, False)])
