@@ -1138,7 +1138,7 @@ def main():
         result["extra"]["stream_ceiling"] = ceiling = stream_ceiling()
         fw_rate = result["fwd_kernel_GBps"]
         result["extra"]["fraction_of_stream_ceiling"] = {
-            "k_event_fwd vs the per-event forward's arrays":
+            "k_event_fwd_rows vs the per-event forward's arrays":
                 round(fw_rate / ceiling["per-event forward's arrays (1:1, 10 units)"]["GB/s"], 4),
             "k_event_bwd vs the per-event backward's arrays":
                 round(achieved / ceiling["per-event backward's arrays (2:1, 15 units)"]["GB/s"], 4)}
