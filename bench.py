@@ -86,7 +86,9 @@ def parse_args():
 class LiteralStep:
     """Preallocated buffers and the C-ABI call list of one fwd+bwd step."""
 
-    def __init__(self, batch: int, channels: int, events: int, seed: int):
+    def __init__(self, batch: int, channels: int, events: int, seed: int, index=None):
+        """`index`: an optional int32 [batch, 256] state index (benchmark config 3) passed to
+        every launch of the step."""
         import torch
 
         from sihc_hip import _lib
@@ -127,6 +129,7 @@ class LiteralStep:
         self.work = [torch.empty((nws + 15) // 16 * 4, device=dev, dtype=torch.float32) for _ in range(E + 1)]
         self.info = (ctypes.c_int * (2 * E + 2))()
         self.stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        self.index = index
         self._build(E)
 
     def _build(self, E):
@@ -138,39 +141,42 @@ class LiteralStep:
         info = lambda k: ctypes.cast(ctypes.addressof(self.info) + 8 * k, ctypes.POINTER(ctypes.c_int))  # noqa: E731
         U = self.M * C * ELEM
         S = self.S
+        # the state index is read once per launch (4 B per token) and counted as such
+        ix = None if self.index is None else p(self.index)
         w_bytes = C * S * ELEM
+        ixb = 0 if self.index is None else self.M * 4
         fwd, bwd = [], []
         # forward
         outs = (vp * 1)(self.z[0].data_ptr())
-        fwd.append(("read", L.sihc_read, (p(self.x[0]), p(self.alpha[0]), outs, 1, B, G, K, C, None, bf16,
-                                           self.stream), (S + 1) * U + w_bytes))
+        fwd.append(("read", L.sihc_read, (p(self.x[0]), p(self.alpha[0]), outs, 1, B, G, K, C, ix, bf16,
+                                           self.stream), (S + 1) * U + w_bytes + ixb))
         for i in range(E):
             last = i == E - 1
             fwd.append(("event_forward_last" if last else "event_forward", L.sihc_event_forward,
                         (p(self.x[i]), p(self.dz[i]), p(self.beta[i]), None if last else p(self.alpha[i + 1]),
-                         p(self.x[i + 1]), None if last else p(self.z[i + 1]), B, G, K, C, None, bf16, self.stream),
-                        ((2 * S + 1) if last else (2 * S + 2)) * U + (1 if last else 2) * w_bytes))
+                         p(self.x[i + 1]), None if last else p(self.z[i + 1]), B, G, K, C, ix, bf16, self.stream),
+                        ((2 * S + 1) if last else (2 * S + 2)) * U + (1 if last else 2) * w_bytes + ixb))
         # backward: last event (write only, carrier gradient aliased), then full events, each
         # with its weight-gradient finalize deferred (sihc_event_backward_partial) ...
         h = self.h_out
         bwd.append(("event_backward_last", L.sihc_event_backward_partial,
                     (p(h), None, None, p(self.dz[E - 1]), p(self.beta[E - 1]), None, None, p(self.gdz[E - 1]),
-                     p(self.gbeta[E - 1]), None, B, G, K, C, None, bf16, bf16, p(self.work[E - 1]), nwork, info(E - 1),
-                     self.stream), (S + 2) * U + 2 * w_bytes))
+                     p(self.gbeta[E - 1]), None, B, G, K, C, ix, bf16, bf16, p(self.work[E - 1]), nwork, info(E - 1),
+                     self.stream), (S + 2) * U + 2 * w_bytes + ixb))
         for i in range(E - 2, -1, -1):
             dst = self.gx[i % 2]
             bwd.append(("event_backward", L.sihc_event_backward_partial,
                         (p(h), p(self.gz[i + 1]), p(self.x[i + 1]), p(self.dz[i]), p(self.beta[i]),
                          p(self.alpha[i + 1]), p(dst), p(self.gdz[i]), p(self.gbeta[i]), p(self.galpha[i + 1]),
-                         B, G, K, C, None, bf16, bf16, p(self.work[i]), nwork, info(i), self.stream),
-                        (3 * S + 3) * U + 4 * w_bytes))
+                         B, G, K, C, ix, bf16, bf16, p(self.work[i]), nwork, info(i), self.stream),
+                        (3 * S + 3) * U + 4 * w_bytes + ixb))
             h = dst
         # adjoint of the first read (no write part): dX_0 = h + alpha_0 (x) g_0, dalpha_0
         dst = self.gx[1] if h is self.gx[0] else self.gx[0]
         bwd.append(("event_backward_first", L.sihc_event_backward_partial,
                     (p(h), p(self.gz[0]), p(self.x[0]), None, None, p(self.alpha[0]), p(dst), None, None,
-                     p(self.galpha[0]), B, G, K, C, None, bf16, bf16, p(self.work[E]), nwork, info(E),
-                     self.stream), (3 * S + 1) * U + 2 * w_bytes))
+                     p(self.galpha[0]), B, G, K, C, ix, bf16, bf16, p(self.work[E]), nwork, info(E),
+                     self.stream), (3 * S + 1) * U + 2 * w_bytes + ixb))
         # ... then every event's dbeta / dalpha in one launch per 32 events (same bits)
         self.finalize_args = None
         bwd.append(("event_finalize", self._finalize, (), 0))
@@ -260,6 +266,44 @@ class LiteralStep:
         b1.record()
         self.run(bt)
         marks.append((f0, f1, fe, b0, b1, len(fb), len(bb)))
+
+
+def measure_step(torch, step: LiteralStep, steps: int, warmup: int) -> dict:
+    """Time `steps` steps back to back after `warmup` untimed ones, bracketed by device
+    synchronisation, with no HIP event inside (an event record between two launches idles
+    the GPU for several microseconds). The average launch times of the full per-event
+    kernels and the phase split come from marked one-stream steps run after it: HIP events
+    there mark only the phase boundaries and the two runs of full per-event launches."""
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        step.step()
+    torch.cuda.synchronize()
+    print(f"[bench] warmup done ({warmup} steps)", file=sys.stderr, flush=True)
+    marks: list = []
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step.step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    spans = []
+    for _ in range(max(2, min(steps, 5))):
+        a, c = ev(), ev()
+        a.record()
+        step.step(marks)
+        c.record()
+        spans.append((a, c))
+    torch.cuda.synchronize()
+    return {
+        "ms_step": wall / steps * 1e3,
+        "marked_ms": statistics.median(a.elapsed_time(c) for a, c in spans),
+        "fwd_kernel_ms": statistics.median(f0.elapsed_time(f1) / nf for f0, f1, _, _, _, nf, _ in marks),
+        "bwd_kernel_ms": statistics.median(b0.elapsed_time(b1) / nb for _, _, _, b0, b1, _, nb in marks),
+        "bwd_launches": sum(mk[6] for mk in marks),
+        # phase split from the step's own events: forward = start .. end of the forward tail
+        "fwd_ms": statistics.median(a.elapsed_time(mk[2]) for (a, _), mk in zip(spans, marks)),
+        "bwd_ms": statistics.median(mk[2].elapsed_time(c) for (_, c), mk in zip(spans, marks)),
+    }
 
 
 def _timed(torch, fn, iters=10, warmup=2):
@@ -474,13 +518,44 @@ def config3_indexed(seed: int) -> dict:
     t_s = _timed(torch, lambda: launch.scatter_cells(cells, idx))
     # the same launches without the index, for the cost of the index at this batch
     t_fu, t_bu = _timed(torch, lambda: fwd3(None), iters=20), _timed(torch, lambda: bwd3(None), iters=20)
-    return {
-        "workload": "batch 128, D=1152, int32 state index (seeded groups of 5), bf16; C-ABI launches on "
-                    "preallocated buffers, backward with its finalize launch",
+    per_call = {
+        "schedule": "one event's forward, then its backward with its own finalize launch (sihc_event_backward), "
+                    "the same buffers every call",
         "event_forward_GB/s": round(10 * U / t_f / 1e9, 1), "event_backward_GB/s": round(15 * U / t_b / 1e9, 1),
         "unindexed_event_forward_GB/s": round(10 * U / t_fu / 1e9, 1),
         "unindexed_event_backward_GB/s": round(15 * U / t_bu / 1e9, 1),
-        "gather_GB/s": round(2 * S * U / t_g / 1e9, 1), "scatter_GB/s": round(2 * S * U / t_s / 1e9, 1),
+    }
+    out = {"gather_GB/s": round(2 * S * U / t_g / 1e9, 1), "scatter_GB/s": round(2 * S * U / t_s / 1e9, 1)}
+    del x, d, h, gz, xo, zo, gx3, gdz3, ws3, cells
+    torch.cuda.empty_cache()
+    # ---- the config-2 step at config 3's shape: 56 events (28 layers x 2 sublayers) on
+    # per-event buffers, the backward as a chain of sihc_event_backward_chain calls, every
+    # launch through the state index; then the same step without it. Per-launch rates are
+    # the span averages of the full per-event launches (measure_step).
+    steps = {}
+    for name, ix in (("indexed", idx), ("unindexed", None)):
+        st = LiteralStep(B, C, 56, seed + 3, index=ix)
+        st.use_chain(True)
+        m = measure_step(torch, st, steps=5, warmup=2)
+        fwd_b = next(c[3] for c in st.fwd if c[0] == "event_forward")
+        bwd_b = next(c[3] for c in st.bwd if c[0] == "event_backward")
+        steps[name] = {"ms_per_step": round(m["ms_step"], 3),
+                       "GB/s": round((st.bytes_fwd + st.bytes_bwd) / (m["ms_step"] * 1e-3) / 1e9, 1),
+                       "tokens_per_s": round(B * 256 / (m["ms_step"] * 1e-3), 1),
+                       "event_forward_GB/s": round(fwd_b / (m["fwd_kernel_ms"] * 1e-3) / 1e9, 1),
+                       "event_backward_GB/s": round(bwd_b / (m["bwd_kernel_ms"] * 1e-3) / 1e9, 1),
+                       "event_backward_avg_ms": round(m["bwd_kernel_ms"], 4)}
+        del st
+        torch.cuda.empty_cache()
+    return {
+        "workload": "batch 128, D=1152, int32 state index (seeded groups of 5), bf16, C-ABI launches on "
+                    "preallocated buffers: the config-2 step's schedule at this shape (56 events, chained "
+                    "backward finalizes; 'step'), and single events with their own finalize launch ('per_call')",
+        "event_forward_GB/s": steps["indexed"]["event_forward_GB/s"],
+        "event_backward_GB/s": steps["indexed"]["event_backward_GB/s"],
+        "unindexed_event_forward_GB/s": steps["unindexed"]["event_forward_GB/s"],
+        "unindexed_event_backward_GB/s": steps["unindexed"]["event_backward_GB/s"],
+        "step": steps, "per_call": per_call, **out,
         "event_fwd_bwd_tokens_per_s": round(B * 256 / (t_f + t_b), 1),
     }
 
@@ -1028,44 +1103,9 @@ def main():
           flush=True)
     step = LiteralStep(args.batch, args.channels, args.events, args.seed)
     step.use_chain(args.finalize == "chain")
-    run_step = step.step
-    torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        run_step()
-    torch.cuda.synchronize()
-    print(f"[bench] warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
-
-    # Timed region: the K steps back to back, bracketed by device synchronisation, with no
-    # HIP event inside (an event record between two launches idles the GPU for several
-    # microseconds). The dominant kernels' average launch times and the phase split come
-    # from marked one-stream steps run after it: HIP events there mark only the phase
-    # boundaries and the two runs of full per-event launches.
-    marks: list = []
-    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        run_step()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = wall / args.steps * 1e3
-    t_fwd = []
-    for _ in range(max(2, min(args.steps, 5))):
-        a, c = ev(), ev()
-        a.record()
-        step.step(marks)
-        c.record()
-        t_fwd.append((a, c))
-    torch.cuda.synchronize()
-    marked_ms = statistics.median(a.elapsed_time(c) for a, c in t_fwd)
-    fwd_kern_ms = [f0.elapsed_time(f1) / nf for f0, f1, _, _, _, nf, _ in marks]
-    kern_ms = [b0.elapsed_time(b1) / nb for _, _, _, b0, b1, _, nb in marks]
-    avg_kernel_ms = statistics.median(kern_ms)
-    avg_fwd_kernel_ms = statistics.median(fwd_kern_ms)
-    n_bwd_launches = sum(m[6] for m in marks)
-    # phase split from the step's own events: forward = start .. end of the forward tail
-    fwd_ms = statistics.median(a.elapsed_time(m[2]) for (a, _), m in zip(t_fwd, marks))
-    bwd_ms = statistics.median(m[2].elapsed_time(c) for (_, c), m in zip(t_fwd, marks))
+    m = measure_step(torch, step, args.steps, args.warmup)
+    ms_step, marked_ms, fwd_ms, bwd_ms = m["ms_step"], m["marked_ms"], m["fwd_ms"], m["bwd_ms"]
+    avg_kernel_ms, avg_fwd_kernel_ms, n_bwd_launches = m["bwd_kernel_ms"], m["fwd_kernel_ms"], m["bwd_launches"]
     print(f"[bench] timed {args.steps} steps: {ms_step:.3f} ms/step", file=sys.stderr, flush=True)
 
     total_bytes = step.bytes_fwd + step.bytes_bwd
