@@ -1371,14 +1371,6 @@ __global__ void __launch_bounds__(256, SIHC_TRIB_MINB) k_trib_waves(const T* __r
       const int e = wave + k * NW;
       if (e < E) emit(acc[k], e);
     }
-  } else if (m_begin >= m_end) {
-    // a chunk past the last token (chunks x tpb can exceed M by more than tpb) still owns
-    // its partial rows: zeros, so the finalize never reads rows nobody wrote
-#pragma unroll
-    for (int k = 0; k < TRIB_MAXK; ++k) {
-      const int e = wave + k * NW;
-      if (e < E) emit(acc[0], e);
-    }
   }
 }
 
@@ -3114,6 +3106,11 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
   int bcg, slices;
   wgrad_block(g.C, V, events, &bcg, &slices);
   const int tpb = int((int64_t(g.M) + chunks - 1) / chunks);
+  // Only chunks that hold tokens are launched and finalized: with tpb rounded up, the last
+  // chunks of max_chunks can lie wholly past the last token (70,000 rows in 1,024 chunks:
+  // 69 rows each, 1,015 chunks), and their partial rows would be read but never written.
+  // (A zero-row branch for them inside k_trib_waves cost that kernel 7%.)
+  if (g.M > 0) chunks = int((int64_t(g.M) + tpb - 1) / tpb);
   // x tile of TT tokens: at most 32 KB of LDS. With 16 or fewer event lanes on the
   // carrier, 8-token tiles keep one round of update loads per tile (measured: E=16
   // 828 -> 766 us at the XL shape; more events or the workspace mode prefer up to 64:
@@ -3172,6 +3169,7 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
             // whole rounds of resident blocks, so the last round is not part-empty
             chunks = whole_rounds(slicesz, max_chunks, resident_blocks(kfn, C16_LANES * nw, ldsz));
             const int tpbz = int((int64_t(g.M) + chunks - 1) / chunks);
+            if (tpbz > 0) chunks = int((int64_t(g.M) + tpbz - 1) / tpbz);  // no chunk past the last token
             if constexpr (D2) {
               hipLaunchKernelGGL((k_wgradz_d2<NPQ, EP>), dim3(blocks1d(slicesz, chunks)), dim3(C16_LANES, nw), ldsz,
                                  st, reinterpret_cast<const bf16_t*>(x), pk, part, index, events, g, tpbz, slicesz);
