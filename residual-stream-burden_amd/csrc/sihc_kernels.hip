@@ -150,7 +150,7 @@
 #define SIHC_K4_DOT2 1
 #endif
 #ifndef SIHC_RDW_MINE  // 4-slot bf16 reads with at least this many events: k_read_w (0: never)
-#define SIHC_RDW_MINE 8
+#define SIHC_RDW_MINE 17  // XL shape: E = 16 k_read 573 vs 582 us, E = 20 743 vs 710, 8-12 equal
 #endif
 #ifndef SIHC_RD2_U  // tokens per lane per iteration of the 16-slot dot2 read
 #define SIHC_RD2_U 4
