@@ -9,6 +9,10 @@ each event's weight-gradient partial rows are summed:
 
 The partial rows and the fixed-order sums are the same in both, so every output
 (carrier and workspace gradients, dbeta, dalpha) must be bit-identical, step after step.
+
+The config-3 step (the same launches through a state index) is checked the same way: with
+the identity index against the step without one, and with a group-of-5 permutation index
+against the step without one over the carrier whose cells are in token order.
 """
 from __future__ import annotations
 
@@ -62,3 +66,50 @@ def test_finalize_schedules_are_bit_identical(batch, events):
         _poison(step)
         step.step()
         _same(_snapshot(step), deferred, f"chain step {r}")
+
+
+def _run(step):
+    _poison(step)
+    step.step()
+    return _snapshot(step)
+
+
+def test_identity_index_step_matches_unindexed():
+    # the config-3 step (every launch through a state index) with the identity index: the
+    # same launches, so the same bits as the step without an index
+    announce("config-3 step, identity index vs no index, batch=3 events=7 D=1152")
+    batch, events = 3, 7
+    ident = torch.arange(256, device="cuda", dtype=torch.int32).repeat(batch, 1)
+    plain = _run(bench.LiteralStep(batch, 1152, events, seed=13))
+    indexed = _run(bench.LiteralStep(batch, 1152, events, seed=13, index=ident))
+    _same(indexed, plain, "identity index")
+
+
+def test_permutation_index_step_matches_unindexed_on_gathered_carrier():
+    # Through a per-image permutation index (the seeded groups of 5), token n of image b
+    # reads and writes cell index[b, n]. The step without an index over the carrier whose
+    # cell n is that cell computes the same per-token values in the same token order, so
+    # every output matches bit for bit: the carriers after gathering their cells, the
+    # workspace outputs and gradients as they are, and the weight gradients (their
+    # partial sums run over the same values in the same order).
+    from sihc_hip import launch
+    from sihc_hip.indexed import group_index
+
+    announce("config-3 step, group-of-5 index vs no index on gathered cells, batch=3 events=7")
+    batch, events = 3, 7
+    idx = group_index(batch, 16, 5, seed=3).cuda()
+    ident = torch.arange(256, device="cuda", dtype=torch.int32).repeat(batch, 1)
+    si = bench.LiteralStep(batch, 1152, events, seed=17, index=idx)
+    su = bench.LiteralStep(batch, 1152, events, seed=17)
+    # the unindexed step's carrier inputs: the indexed step's cells in token order
+    in_token_order = lambda t: launch.scatter_cells(launch.gather_cells(t, idx, 4), ident)  # noqa: E731
+    with torch.no_grad():
+        su.x[0].copy_(in_token_order(si.x[0]))
+        su.h_out.copy_(in_token_order(si.h_out))
+    a, b = _run(si), _run(su)
+    cells = lambda t, ix: launch.gather_cells(t, ix, 4)  # noqa: E731
+    assert torch.equal(cells(a["x_last"], idx), cells(b["x_last"], ident)), "carrier after the last event"
+    for x, y in zip(a["gx"], b["gx"]):
+        assert torch.equal(cells(x, idx), cells(y, ident)), "carrier gradient"
+    for k in ("z1", "gdz0", "gdz_last", "gbeta", "galpha"):
+        assert torch.equal(a[k], b[k]), k
