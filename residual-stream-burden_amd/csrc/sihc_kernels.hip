@@ -2742,10 +2742,14 @@ Shape2D shape_for(int C, int V, int bcg0, int lds_per_channel, int lds_cap = 64 
 // into LDS; with 16-slot cells that staging is large enough that blocks must cover more
 // tokens as E grows (measured at batch 256, D 1152: E = 24 read 1872 -> 1624 us with
 // 64 tokens per lane, while E = 1 is fastest with 8).
-int rw_tokens_per_lane(int cell, int events, bool read = false) {
+int rw_tokens_per_lane(int cell, int events, bool read = false, bool dot2_read = false) {
   // 4-slot reads: 32-token blocks (64 with one event) stream through a narrower window
   // than 128-token ones (E = 2..16: 6-7% faster)
   if (cell == 2) return read ? (events == 1 ? 4 : 2) : SIHC_RW_TPT;
+  // 16-slot bf16 reads on k_read_d2 (packed weights, cheap to stage): short blocks past 12
+  // events (XL shape: E = 16 957 -> 929 us with 8 tokens, E = 24 1251 -> 1206 us with 16,
+  // E = 32 2210 -> 2078; 3-12 events do not care)
+  if (dot2_read && events > 12) return events <= 16 ? 8 : 16;
   // 16 slots: the weight slice staged per block grows with E, so blocks grow too; with
   // hinted loads and stores reads with 3-12 events and writes with 9-12 gain from twice
   // the tokens again (read E = 8: 794 -> 745 us), 1-2 and 13+ events do not
@@ -3361,7 +3365,7 @@ int sihc_read(const void* x, const void* alpha, void* const* out, int events, in
   }
   const Shape2D sh = cell == 2 ? shape_for(channels, V, SIHC_RW_BCG, events * S * wbytes)
                                : shape_for(channels, V, SIHC_RW_BCG_K4, events * S * wbytes, SIHC_RW_LDS_K4);
-  const int tpb = sh.tl * rw_tokens_per_lane(cell, events, true);
+  const int tpb = sh.tl * rw_tokens_per_lane(cell, events, true, d2 && V == 2);
   const int64_t chunks = (int64_t(g.M) + tpb - 1) / tpb;
   const int gs = tpb;  // one contiguous run per block (interleaved groups measured no faster)
   const size_t lds = size_t(events) * S * sh.bcg * V * wbytes;
