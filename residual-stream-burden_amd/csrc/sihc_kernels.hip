@@ -2745,7 +2745,9 @@ Shape2D shape_for(int C, int V, int bcg0, int lds_per_channel, int lds_cap = 64 
 int rw_tokens_per_lane(int cell, int events, bool read = false, bool dot2_read = false) {
   // 4-slot reads: 32-token blocks (64 with one event) stream through a narrower window
   // than 128-token ones (E = 2..16: 6-7% faster)
-  if (cell == 2) return read ? (events == 1 ? 4 : 2) : SIHC_RW_TPT;
+  // 4-slot writes: 4 tokens per lane from 4 events (XL shape: E = 8 426 -> 417 us, E = 16
+  // 655 -> 647, E = 24 889 -> 883; fewer events measured the same as with 8)
+  if (cell == 2) return read ? (events == 1 ? 4 : 2) : (events >= 4 ? 4 : SIHC_RW_TPT);
   // 16-slot bf16 reads on k_read_d2 (packed weights, cheap to stage): short blocks past 12
   // events (XL shape: E = 16 957 -> 929 us with 8 tokens, E = 24 1251 -> 1206 us with 16,
   // E = 32 2210 -> 2078; 3-12 events do not care)
