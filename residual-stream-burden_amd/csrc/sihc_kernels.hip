@@ -167,6 +167,9 @@
 #ifndef SIHC_WG_CHUNK  // tokens per reduction chunk, weight / gamma gradients
 #define SIHC_WG_CHUNK 512
 #endif
+#ifndef SIHC_WG_CHUNK_K4  // the same for 16-slot carriers (XL shape, E = 24: 1214 -> 1163 us against 512)
+#define SIHC_WG_CHUNK_K4 1024
+#endif
 #ifndef SIHC_WG_PAD  // most idle event lanes added to make k_wgrad blocks 4 whole waves
 #define SIHC_WG_PAD 4
 #endif
@@ -1585,7 +1588,7 @@ __global__ void __launch_bounds__(512) k_wgrad16(const T* __restrict__ x, PtrPac
 }
 
 // Pipelined carrier weight gradient (4- and 16-slot cells) for bf16 rows of whole
-// 16-byte vectors and 8+ events. A lane owns ONE channel and EPL events (EPL x S
+// 16-byte vectors and up to 24 events. A lane owns ONE channel and EPL events (EPL x S
 // accumulators). The update rows join the carrier tile in LDS (16-byte loads: each wave
 // stages whole 64-channel rows of its own events, so the update pointer stays
 // wave-uniform), and the loads of tile k+1 are issued into registers before tile k is
@@ -2784,12 +2787,12 @@ void wgrad_block(int C, int V, int events, int* bcg_out, int* slices_out) {
 // (few events give small blocks), with at least 32 tokens per chunk. A function of the
 // sizes only (the block shape is taken at the widest vector), so the workspace size is
 // known before the pointers are.
-int wgrad_chunks(int64_t M, int events, int C) {
+int wgrad_chunks(int64_t M, int events, int C, int cell = 2) {
   int bcg, slices;
   wgrad_block(C, 8, std::max(events, 1), &bcg, &slices);
   const int64_t waves_per_chunk = int64_t(slices) * ((bcg * std::max(events, 1) + 63) / 64);
   const int64_t want = (4096 + waves_per_chunk - 1) / waves_per_chunk;
-  const int base = chunk_count(M, SIHC_WG_CHUNK, 128);
+  const int base = chunk_count(M, cell == 4 ? SIHC_WG_CHUNK_K4 : SIHC_WG_CHUNK, 128);
   const int64_t cap = std::max<int64_t>(1, std::min<int64_t>(M / 32, 2048));
   return int(std::max<int64_t>(base, std::min(want, cap)));
 }
@@ -3095,7 +3098,7 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
                  int S, bool carrier, const int32_t* index, int dtype, int out_dtype, void* workspace,
                  size_t workspace_bytes, hipStream_t st, void* const* dout = nullptr, const void* gamma = nullptr,
                  int gamma_dtype = SIHC_DTYPE_F32) {
-  const int max_chunks = dout ? trib_chunks(g.M, events, g.C) : wgrad_chunks(g.M, events, g.C);
+  const int max_chunks = dout ? trib_chunks(g.M, events, g.C) : wgrad_chunks(g.M, events, g.C, carrier ? g.K : 2);
   int chunks = max_chunks;  // k_wgradz may use fewer (whole rounds of resident blocks)
   const size_t need = size_t(max_chunks) * events * S * g.C * sizeof(float);
   if (!workspace || workspace_bytes < need)
@@ -3138,9 +3141,9 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
   // 16-slot carrier: k_wgrad16 (one channel per lane); only x is loaded as vectors
   const int slices16 = (g.C + C16_LANES - 1) / C16_LANES;
   const int vs16 = pick_vec(g.C, es, 8, &x, 1);
-  // pipelined k_wgradz: bf16, 8..24 events, every row of x and the updates in whole
+  // pipelined k_wgradz: bf16, up to 24 events, every row of x and the updates in whole
   // 16-byte vectors (C % 8 == 0, 16-byte aligned pointers)
-  const bool usez = SIHC_C16Z && dtype == SIHC_DTYPE_BF16 && events >= 8 && events <= 24 && !dout &&
+  const bool usez = SIHC_C16Z && dtype == SIHC_DTYPE_BF16 && events <= 24 && !dout &&
                     pick_vec(g.C, es, 8, ptrs, nptr) == 8;
   const int slicesz = (g.C + C16_LANES - 1) / C16_LANES;
   float* part = static_cast<float*>(workspace);
@@ -3192,7 +3195,13 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
           };
           const bool bf = std::is_same<T, bf16_t>::value && usez;
           if constexpr (CAR && KK == 4) {
-            if (bf) {
+            if (bf && events < 8) {
+              // few events: 4 waves of one event (idle waves only stage the carrier tile)
+              // or 2 waves of 4; every event row staged (waves x events per lane >= E) and
+              // the 1024-vector carrier tile covered (threads x vectors per thread)
+              if (events <= 4) goz(IC<4>{}, IC<4>{}, IC<1>{}, 4);
+              else goz(IC<4>{}, IC<8>{}, IC<4>{}, 2);
+            } else if (bf) {
               // 16 slots: 3 events per lane where that balances the SIMDs, else 4 with
               // 2..8 waves; carrier vectors per thread = 1024 / (64 * waves), rounded up
               if (balanced_epl({4, 3}) == 3) {
@@ -3212,6 +3221,11 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
               hipLaunchKernelGGL((k_wgrad16<T>), dim3(blocks1d(slices16, chunks)), dim3(C16_LANES, nw), 0, st,
                                  static_cast<const T*>(x), pk, part, index, events, g, tpb, slices16, vs16);
             }
+          } else if (CAR && KK == 2 && bf && SIHC_WGZ_K2 && events >= 2 && events < 8 && !balanced_epl({2})) {
+            // 4 slots, 2..6 events: 4 waves of 1 or 2 events (the 256-vector carrier tile,
+            // one vector per thread); one event keeps its direct kernel
+            if (events <= 4) goz(IC<2>{}, IC<1>{}, IC<1>{}, 4);
+            else goz(IC<2>{}, IC<1>{}, IC<2>{}, 4);
           } else if (CAR && KK == 2 && bf && SIHC_WGZ_K2 && balanced_epl({6, 4, 3, 2})) {
             // 4 slots, only where the waves balance (4 or 8 waves: 1 carrier vector each)
             const int ep = balanced_epl({6, 4, 3, 2}), nw = (events + ep - 1) / ep;
@@ -3514,7 +3528,7 @@ int sihc_write(const void* x, const void* const* updates, const void* beta, void
 size_t sihc_weight_grad_workspace_size(int events, int64_t batch, int grid, int cell, int channels) {
   if (events < 1 || batch < 0 || grid <= 0 || cell <= 0 || channels <= 0) return 0;
   const int64_t M = batch * int64_t(grid) * grid;
-  return size_t(wgrad_chunks(M, events, channels)) * events * cell * cell * channels * sizeof(float);
+  return size_t(wgrad_chunks(M, events, channels, cell)) * events * cell * cell * channels * sizeof(float);
 }
 
 int sihc_weight_grad(const void* x, const void* const* z, void* out, int events, int64_t batch, int grid, int cell,
