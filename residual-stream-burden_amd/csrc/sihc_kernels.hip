@@ -1588,18 +1588,18 @@ __global__ void __launch_bounds__(512) k_wgrad16(const T* __restrict__ x, PtrPac
 }
 
 // Pipelined carrier weight gradient (4- and 16-slot cells) for bf16 rows of whole
-// 16-byte vectors and up to 24 events. A lane owns ONE channel and EPL events (EPL x S
+// 16-byte vectors and up to 32 events. A lane owns ONE channel and EPL events (EPL x S
 // accumulators). The update rows join the carrier tile in LDS (16-byte loads: each wave
 // stages whole 64-channel rows of its own events, so the update pointer stays
 // wave-uniform), and the loads of tile k+1 are issued into registers before tile k is
 // reduced, so every tile's HBM latency overlaps the previous tile's arithmetic. Tokens
 // are summed in ascending order, as in k_wgrad16 and k_wgrad: for the same chunks the
 // partial rows are identical bit for bit.
-// NXQ = carrier vectors staged per thread (TT * S * 8 / threads, rounded up); EPL is
-// chosen so that the wave count is a multiple of 4 where possible: the 4 SIMDs of a CU
-// then hold equal shares of each block (16 slots, E = 24: 6 waves of 4 events 2031 us,
-// 8 waves of 3 events 1528 us at batch 256, D 1152).
-#ifndef SIHC_WGZ_K2  // 1: 4-slot carriers also use k_wgradz where its waves balance
+// NXQ = carrier vectors staged per thread (TT * S * 8 / threads, rounded up); the waves
+// and EPL per event count come from measurements (launch_wgrad): 4 or 8 waves where they
+// divide the events well (16 slots, E = 24: 6 waves of 4 events 2031 us, 8 waves of 3
+// events 1528 us at batch 256, D 1152), else the fastest measured shape.
+#ifndef SIHC_WGZ_K2  // 1: 4-slot carriers also use k_wgradz (from 2 events)
 #define SIHC_WGZ_K2 1
 #endif
 #ifndef SIHC_C16Z_MINW  // minimum waves per SIMD k_wgradz is compiled for
@@ -3141,9 +3141,9 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
   // 16-slot carrier: k_wgrad16 (one channel per lane); only x is loaded as vectors
   const int slices16 = (g.C + C16_LANES - 1) / C16_LANES;
   const int vs16 = pick_vec(g.C, es, 8, &x, 1);
-  // pipelined k_wgradz: bf16, up to 24 events, every row of x and the updates in whole
+  // pipelined k_wgradz: bf16, up to 32 events, every row of x and the updates in whole
   // 16-byte vectors (C % 8 == 0, 16-byte aligned pointers)
-  const bool usez = SIHC_C16Z && dtype == SIHC_DTYPE_BF16 && events <= 24 && !dout &&
+  const bool usez = SIHC_C16Z && dtype == SIHC_DTYPE_BF16 && events <= 32 && !dout &&
                     pick_vec(g.C, es, 8, ptrs, nptr) == 8;
   const int slicesz = (g.C + C16_LANES - 1) / C16_LANES;
   float* part = static_cast<float*>(workspace);
@@ -3187,52 +3187,37 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
                                  st, reinterpret_cast<const bf16_t*>(x), pk, part, index, events, g, tpbz, slicesz);
             }
           };
-          // events per lane: the first candidate giving 4 or 8 event waves (0: none)
-          auto balanced_epl = [&](std::initializer_list<int> cands) {
-            for (int ep : cands)
-              if ((events + ep - 1) / ep == 4 || (events + ep - 1) / ep == 8) return ep;
-            return 0;
-          };
           const bool bf = std::is_same<T, bf16_t>::value && usez;
+          // Shapes of the pipelined kernel (waves x events per lane), measured per event count
+          // at the XL shape (batch 256, D 1152). Every shape stages every event row (waves x
+          // events per lane >= E) and covers the carrier tile (64 x waves x vectors per
+          // thread >= 256 vectors at 4 slots, 1024 at 16).
           if constexpr (CAR && KK == 4) {
-            if (bf && events < 8) {
-              // few events: 4 waves of one event (idle waves only stage the carrier tile)
-              // or 2 waves of 4; every event row staged (waves x events per lane >= E) and
-              // the 1024-vector carrier tile covered (threads x vectors per thread)
-              if (events <= 4) goz(IC<4>{}, IC<4>{}, IC<1>{}, 4);
-              else goz(IC<4>{}, IC<8>{}, IC<4>{}, 2);
-            } else if (bf) {
-              // 16 slots: 3 events per lane where that balances the SIMDs, else 4 with
-              // 2..8 waves; carrier vectors per thread = 1024 / (64 * waves), rounded up
-              if (balanced_epl({4, 3}) == 3) {
-                const int nw = (events + 2) / 3;
-                if (nw == 4) goz(IC<4>{}, IC<4>{}, IC<3>{}, nw);
-                else goz(IC<4>{}, IC<2>{}, IC<3>{}, nw);
-              } else {
-                const int nw = (events + 3) / 4;
-                if (nw == 2) goz(IC<4>{}, IC<8>{}, IC<4>{}, nw);
-                else if (nw == 3) goz(IC<4>{}, IC<6>{}, IC<4>{}, nw);
-                else if (nw <= 5) goz(IC<4>{}, IC<4>{}, IC<4>{}, nw);
-                else if (nw <= 7) goz(IC<4>{}, IC<3>{}, IC<4>{}, nw);
-                else goz(IC<4>{}, IC<2>{}, IC<4>{}, nw);
-              }
+            if (bf) {
+              // 16 slots: E = 9 3 x 3 730 us (2 x 5 of 4: 907), E = 17-21 8 x 3 1095-1142 us
+              // (5-6 x 4: 1320-1429), E = 28 / 32 8 x 4 1405 / 1421 us (k_wgrad16: 2290 / 2089)
+              if (events <= 4) goz(IC<4>{}, IC<4>{}, IC<1>{}, 4);        // idle waves only stage
+              else if (events <= 8) goz(IC<4>{}, IC<8>{}, IC<4>{}, 2);
+              else if (events == 9) goz(IC<4>{}, IC<6>{}, IC<3>{}, 3);
+              else if (events <= 12) goz(IC<4>{}, IC<4>{}, IC<3>{}, 4);
+              else if (events <= 16) goz(IC<4>{}, IC<4>{}, IC<4>{}, 4);
+              else if (events <= 24) goz(IC<4>{}, IC<2>{}, IC<3>{}, 8);
+              else goz(IC<4>{}, IC<2>{}, IC<4>{}, 8);
             } else {
               const int nw = (events + C16_EPL - 1) / C16_EPL;
               hipLaunchKernelGGL((k_wgrad16<T>), dim3(blocks1d(slices16, chunks)), dim3(C16_LANES, nw), 0, st,
                                  static_cast<const T*>(x), pk, part, index, events, g, tpb, slices16, vs16);
             }
-          } else if (CAR && KK == 2 && bf && SIHC_WGZ_K2 && events >= 2 && events < 8 && !balanced_epl({2})) {
-            // 4 slots, 2..6 events: 4 waves of 1 or 2 events (the 256-vector carrier tile,
-            // one vector per thread); one event keeps its direct kernel
-            if (events <= 4) goz(IC<2>{}, IC<1>{}, IC<1>{}, 4);
-            else goz(IC<2>{}, IC<1>{}, IC<2>{}, 4);
-          } else if (CAR && KK == 2 && bf && SIHC_WGZ_K2 && balanced_epl({6, 4, 3, 2})) {
-            // 4 slots, only where the waves balance (4 or 8 waves: 1 carrier vector each)
-            const int ep = balanced_epl({6, 4, 3, 2}), nw = (events + ep - 1) / ep;
-            if (ep == 6) goz(IC<2>{}, IC<1>{}, IC<6>{}, nw);
-            else if (ep == 4) goz(IC<2>{}, IC<1>{}, IC<4>{}, nw);
-            else if (ep == 3) goz(IC<2>{}, IC<1>{}, IC<3>{}, nw);
-            else goz(IC<2>{}, IC<1>{}, IC<2>{}, nw);
+          } else if (CAR && KK == 2 && bf && SIHC_WGZ_K2 && events >= 2) {
+            // 4 slots (one event keeps its direct kernel): E = 3 4 x 1 201 us (k_wgrad: 504),
+            // E = 9 3 x 3 355 us (k_wgrad: 622), E = 16 6 x 3 526 us (4 x 4: 573), E = 17-18
+            // 6 x 3 558-573 us (k_wgrad: 933-941), E = 28 7 x 4 923 us (k_wgrad: 1000)
+            if (events <= 4) goz(IC<2>{}, IC<1>{}, IC<1>{}, 4);           // idle waves only stage
+            else if (events <= 8) goz(IC<2>{}, IC<1>{}, IC<2>{}, 4);
+            else if (events == 9) goz(IC<2>{}, IC<2>{}, IC<3>{}, 3);
+            else if (events <= 18) goz(IC<2>{}, IC<1>{}, IC<3>{}, (events + 2) / 3);
+            else if (events <= 24) goz(IC<2>{}, IC<1>{}, IC<6>{}, 4);
+            else goz(IC<2>{}, IC<1>{}, IC<4>{}, (events + 3) / 4);
           } else {
             if (events <= 2) {
               // fused triangular backward: 1 update hints loads only, 2 updates stores

@@ -1,10 +1,9 @@
 """GPU: the carrier weight gradient over every launch shape of its bf16 kernels.
 
-bf16 carriers with rows of whole 16-byte vectors and up to 24 events take the pipelined
-kernel (one channel per lane, EPL events per lane, 2..8 event waves; under 8 events 4
-waves of 1 or 2 events, or 2 waves of 4 at 16 slots); other event counts (4 slots: 1
-event, and counts with no balanced shape), channel counts that are not multiples of 8
-and fp32 take the other kernels.
+bf16 carriers with rows of whole 16-byte vectors and up to 32 events take the pipelined
+kernel (one channel per lane, EPL events per lane, 2..8 event waves chosen per event
+count); one event at 4 slots, channel counts that are not multiples of 8 and fp32 take
+the other kernels.
 Products of bf16 values are exact in fp32 and the sums are fp32, so the fp32 bar applies
 against the oracle's float64 sums of the same bf16 inputs. Token tails (grids of 5x5
 cells), channel tails (136 = 2 x 64 + 8 channels; 24 channels in one 64-lane slice) and
@@ -21,34 +20,35 @@ from sihc_hip import launch
 
 pytestmark = pytest.mark.gpu
 
-# (slots, events): events per lane x waves of the pipelined kernel, or the other kernel
-CASES = [
+CASES = [  # (slots, events): waves x events per lane of the pipelined kernel
     (4, 1),    # the direct kernel
-    (4, 2),    # 1 x 4 (two waves stage only)
-    (4, 4),    # 1 x 4
-    (4, 5),    # 2 x 4 (last wave partly empty)
-    (4, 6),    # 2 x 4
-    (4, 7),    # 2 x 4
-    (4, 8),    # 2 x 4
-    (4, 9),    # no balanced shape: the LDS-tile kernel
-    (4, 12),   # 3 x 4
-    (4, 16),   # 4 x 4
-    (4, 17),   # the LDS-tile kernel
-    (4, 20),   # 6 x 4 (last wave partly empty)
-    (4, 24),   # 6 x 4
-    (16, 1),   # 1 x 4 (three waves stage only)
-    (16, 3),   # 1 x 4
-    (16, 4),   # 1 x 4
-    (16, 5),   # 4 x 2 (last wave partly empty)
-    (16, 7),   # 4 x 2
-    (16, 8),   # 4 x 2
-    (16, 9),   # 4 x 3
-    (16, 12),  # 3 x 4
+    (4, 2),    # 4 x 1 (two waves stage only)
+    (4, 4),    # 4 x 1
+    (4, 5),    # 4 x 2 (last wave partly empty)
+    (4, 7),    # 4 x 2
+    (4, 8),    # 4 x 2
+    (4, 9),    # 3 x 3 (two vectors per thread)
+    (4, 12),   # 4 x 3
+    (4, 13),   # 5 x 3
+    (4, 16),   # 6 x 3
+    (4, 17),   # 6 x 3
+    (4, 20),   # 4 x 6
+    (4, 24),   # 4 x 6
+    (4, 25),   # 7 x 4
+    (4, 32),   # 8 x 4
+    (16, 1),   # 4 x 1 (three waves stage only)
+    (16, 4),   # 4 x 1
+    (16, 5),   # 2 x 4
+    (16, 8),   # 2 x 4
+    (16, 9),   # 3 x 3
+    (16, 12),  # 4 x 3
+    (16, 13),  # 4 x 4
     (16, 16),  # 4 x 4
-    (16, 20),  # 4 x 5
-    (16, 21),  # 4 x 6
-    (16, 24),  # 3 x 8
-    (16, 25),  # the one-channel-per-lane kernel
+    (16, 17),  # 8 x 3
+    (16, 21),  # 8 x 3
+    (16, 24),  # 8 x 3
+    (16, 25),  # 8 x 4
+    (16, 32),  # 8 x 4
 ]
 GEOMS = [(2, 16, 64, False), (3, 5, 136, True), (1, 16, 1152, True), (2, 4, 24, False)]
 
