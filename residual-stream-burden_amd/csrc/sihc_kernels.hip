@@ -161,9 +161,9 @@
 #ifndef SIHC_K2_BF16W  // the same for 4-slot read / write (8-channel lanes)
 #define SIHC_K2_BF16W 1
 #endif
-#ifndef SIHC_RW_LDS_K4  // LDS bytes per block for staged weights, 16 slots
-#define SIHC_RW_LDS_K4 (48 * 1024)
-#endif
+#ifndef SIHC_RW_LDS_K4  // LDS bytes per block for staged weights, 16 slots (of 160 KB per CU):
+#define SIHC_RW_LDS_K4 (80 * 1024)  // 32 channel lanes up to 32 events (48 KB: 16 lanes past 24
+#endif                              // events, read E = 28 1916 -> 1406 us, write 2290 -> 2129)
 #ifndef SIHC_WG_CHUNK  // tokens per reduction chunk, weight / gamma gradients
 #define SIHC_WG_CHUNK 512
 #endif
