@@ -3218,6 +3218,18 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
             else if (events <= 18) goz(IC<2>{}, IC<1>{}, IC<3>{}, (events + 2) / 3);
             else if (events <= 24) goz(IC<2>{}, IC<1>{}, IC<6>{}, 4);
             else goz(IC<2>{}, IC<1>{}, IC<4>{}, (events + 3) / 4);
+          } else if (!CAR && !SD && bf && events >= 2 && events <= 16) {
+            // gamma gradient (one-slot workspace rows, 64-vector tile: one per thread of a
+            // wave) on the pipelined kernel, shapes measured per update count at 65,536 rows x
+            // 1152 channels: A = 3 1 x 3 105 us (LDS-tile kernel: 150), A = 5 1 x 6 150 (187),
+            // A = 8 4 x 2 218 (247), A = 10 2 x 6 275 (305); past 16 the LDS-tile kernel is as fast
+            if (events == 2) goz(IC<1>{}, IC<1>{}, IC<2>{}, 1);
+            else if (events == 3) goz(IC<1>{}, IC<1>{}, IC<3>{}, 1);
+            else if (events == 4) goz(IC<1>{}, IC<1>{}, IC<4>{}, 1);
+            else if (events <= 6) goz(IC<1>{}, IC<1>{}, IC<6>{}, 1);
+            else if (events <= 8) goz(IC<1>{}, IC<1>{}, IC<2>{}, 4);
+            else if (events <= 12) goz(IC<1>{}, IC<1>{}, IC<6>{}, 2);
+            else goz(IC<1>{}, IC<1>{}, IC<8>{}, 2);
           } else {
             if (events <= 2) {
               // fused triangular backward: 1 update hints loads only, 2 updates stores

@@ -74,3 +74,23 @@ def test_carrier_weight_grad_bf16(slots, events, geom):
     assert_parity(got, exp, torch.float32, what=f"wgrad slots={slots} events={events}")
     # deterministic: a second call gives the same bits
     assert torch.equal(got, launch.weight_grad(x, ups, w, index=idx, out_dtype=torch.float32))
+
+
+GAMMA_CASES = [2, 3, 4, 5, 6, 7, 8, 9, 12, 13, 16, 17]  # waves x updates per lane: 1 x A ... 2 x 8; 17: LDS tile
+
+
+@pytest.mark.parametrize("active", GAMMA_CASES)
+@pytest.mark.parametrize("rows,channels", [(3 * 13 * 13, 136), (4096, 1152), (77, 24)],
+                         ids=["r507-c136", "r4096-c1152", "r77-c24"])
+def test_gamma_grad_bf16(active, rows, channels):
+    # the gamma gradient of the triangular op over bf16 workspace rows: sum over rows of
+    # grad * update_j, one slot per row, on the same pipelined kernel (2..16 updates)
+    announce(f"gamma grad bf16 A={active} rows={rows} C={channels}")
+    torch.manual_seed(5 * active + channels)
+    grad = torch.randn(1, rows, channels, device="cuda").to(torch.bfloat16)
+    ups = [torch.randn(1, rows, channels, device="cuda").to(torch.bfloat16) for _ in range(active)]
+    gamma = 0.05 * torch.randn(active, channels, device="cuda")
+    got = launch.triangular_gamma_grad(grad, ups, gamma, out_dtype=torch.float32)
+    exp = O.triangular_gamma_grad(grad.cpu(), [u.cpu() for u in ups])
+    assert_parity(got, exp, torch.float32, what=f"dgamma A={active}")
+    assert torch.equal(got, launch.triangular_gamma_grad(grad, ups, gamma, out_dtype=torch.float32))
