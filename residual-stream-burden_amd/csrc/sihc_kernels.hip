@@ -174,7 +174,7 @@
 #define SIHC_WG_PAD 4
 #endif
 #ifndef SIHC_TRIB_WAVES  // fused triangular backward: k_trib_waves from this many updates (0: never)
-#define SIHC_TRIB_WAVES 4
+#define SIHC_TRIB_WAVES 3  // A = 3: 229 -> 224 us against the LDS-tile kernel (XL shape)
 #endif
 #ifndef SIHC_TRIB_CHUNK  // tokens per reduction chunk, fused triangular backward
 #define SIHC_TRIB_CHUNK 64

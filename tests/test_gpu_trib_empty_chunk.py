@@ -1,11 +1,12 @@
 """GPU: the fused triangular backward when the reduction's last chunk holds no token.
 
-Token chunks are ceil(rows / chunks) long, so for some row counts the last chunk starts
-past the last row (1,250 rows in 39 chunks of 33: 38 x 33 >= 1,250). That chunk must
-still write its partial rows (zeros): the finalize sums every chunk. The workspace is
-filled with NaN before the call, so a row left unwritten shows up in the gamma gradient.
-Shapes take the wave-per-update kernel with one sub-tile per chunk (4+ updates, 16-byte
-bf16 vectors, at most 64 rows per chunk).
+Token chunks are ceil(rows / chunks) long, so for some row counts the last chunks would
+start past the last row (1,250 rows in 39 chunks of 33: 38 x 33 >= 1,250). The host
+launches and finalizes only the chunks that hold rows, so no partial row is summed that
+no block wrote. The workspace is filled with NaN before the call, so a row left unwritten
+(or summed without being written) shows up in the gamma gradient. Shapes take the
+wave-per-update kernel with one sub-tile per chunk (3+ updates, 16-byte bf16 vectors, at
+most 64 rows per chunk).
 """
 from __future__ import annotations
 
