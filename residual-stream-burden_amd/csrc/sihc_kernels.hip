@@ -2979,7 +2979,9 @@ int write_hints(bool whole_line, int events) {
   return events <= 2 ? 2 : 3;  // E <= 2: stores only (4-5%); more events: both (3-7%)
 }
 int triangular_hints(int active) {
-  return active <= 2 ? 2 : active <= 6 ? 3 : 1;  // stores, both, then loads only (A >= 12: both +4%)
+  // stores only for 1-2 updates, then loads and stores (XL shape: A = 9 296 -> 270 us,
+  // A = 23 652 -> 603 against loads only; 3-6 updates equal)
+  return active <= 2 ? 2 : 3;
 }
 
 // 1-D grid of slices x chunks (slices fastest: concurrently resident blocks cover whole
