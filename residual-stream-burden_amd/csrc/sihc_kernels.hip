@@ -441,6 +441,27 @@ __device__ __forceinline__ int logical_block() {
   return logical_block_of<XCD>(int(gridDim.x));
 }
 
+// (slice, chunk) of block blk in a slices-fastest grid, the slice rotated by the chunk. The
+// hardware deals consecutive blocks to the 8 XCDs in turn, so with the plain order a slice
+// count that shares factors with 8 pins each XCD to a few slices of every row (C = 1024 in
+// 128-channel slices: XCD x always takes slice x) and its traffic to a fixed part of every
+// 2 KB row; the per-event backward ran 366.6 against 349.0 us at C = 1024 and 746 against
+// 684 at C = 2048 (C = 1152, 9 slices: the same). Each chunk still runs every slice once,
+// so the partial rows and all sums are unchanged.
+__device__ __forceinline__ void slice_chunk(int blk, int nslices, int& slice, int& chunk) {
+  chunk = blk / nslices;
+  slice = (blk - chunk * nslices + chunk) % nslices;
+}
+// The same, rotated only for slice counts that are not a multiple of 8: the 4-slot read and
+// weight gradient ran slower rotated at C = 1024 (8 / 16 slices: read E = 24 727 -> 759 us,
+// gradient E = 16 532 -> 550) and faster at 768, 1152 and 1280 (gradient E = 16 673 -> 653 at
+// 1280, read E = 24 812 -> 797 at 1152).
+__device__ __forceinline__ void slice_chunk_unless8(int blk, int nslices, int& slice, int& chunk) {
+  chunk = blk / nslices;
+  const int r = blk - chunk * nslices;
+  slice = (nslices & 7) == 0 ? r : (r + chunk) % nslices;
+}
+
 // Carrier pixel of slot 0 of the cell token m reads/writes. Token m = b*GG + n owns
 // cell n of batch b, or cell index[m] in the spatially indexed variant.
 // cell_pixel0_at: the same with the cell already known (`cell` = the clamped index[m]
@@ -1004,7 +1025,9 @@ __global__ void __launch_bounds__(256) k_read_w(const bf16_t* __restrict__ x, co
   extern __shared__ __align__(16) unsigned char smem_rw[];
   uint32_t* xp = reinterpret_cast<uint32_t*>(smem_rw);  // [RDW_TT][2][BC] pair words
   uint32_t* ap = xp + RDW_TT * 2 * BC;                   // [E][2][BC] pair words
-  const int blk = int(blockIdx.x), slice = blk % nslices, chunk = blk / nslices;
+  const int blk = int(blockIdx.x);
+  int slice, chunk;
+  slice_chunk_unless8(blk, nslices, slice, chunk);
   const int cs = slice * BC;
   const int tid = int(threadIdx.x), wave = tid / 64, lane = tid % 64;
   const int lx = lane % LX, ly = lane / LX;
@@ -1115,7 +1138,9 @@ __global__ void __launch_bounds__(256) k_wgrad(const T* __restrict__ x, PtrPack 
   extern __shared__ float xt[];  // [TT*S rows][BCG*V], lds_w layout
   const int BCG = blockDim.x;
   const int BC = BCG * V;
-  const int blk = logical_block<false>(), slice = blk % nslices, chunk = blk / nslices;
+  const int blk = logical_block<false>();
+  int slice, chunk;
+  slice_chunk(blk, nslices, slice, chunk);
   const int cs = slice * BC;
   const int cg = threadIdx.x;
   // event lanes past E (padding to whole 4-wave blocks) only help stage the tile
@@ -1257,7 +1282,9 @@ __global__ void __launch_bounds__(256, SIHC_TRIB_MINB) k_trib_waves(const T* __r
   float* gt = lds;                 // [TRIB_TT][BC] gradient rows
   float* gm = lds + TRIB_TT * BC;  // [E][BC] gamma slice
   const int NW = int(blockDim.x) / 64;
-  const int blk = int(blockIdx.x), slice = blk % nslices, chunk = blk / nslices;
+  const int blk = int(blockIdx.x);
+  int slice, chunk;
+  slice_chunk(blk, nslices, slice, chunk);
   const int cs = slice * BC;
   const int tid = int(threadIdx.x), wave = tid / 64, lane = tid % 64;
   const int lx = lane % LX, ly = lane / LX;
@@ -1397,6 +1424,7 @@ __global__ void __launch_bounds__(256) k_wgrad_direct(const T* __restrict__ x, P
   constexpr int TG = CARRIER ? 2 : 4;
   static_assert(!(STORE_D && CARRIER), "update gradients exist only in workspace mode");
   static_assert(S <= 4, "direct path is for the 4-slot carrier and the workspace");
+  // plain order: rotated, one event at D = 1152 ran 136.5 -> 139.9 us (1024: 130.9 -> 125.7)
   const int blk = logical_block<false>(), slice = blk % nslices, chunk = blk / nslices;
   const int e = threadIdx.y;
   const int c0 = (slice * blockDim.x + threadIdx.x) * V;
@@ -1534,7 +1562,9 @@ __global__ void __launch_bounds__(512) k_wgrad16(const T* __restrict__ x, PtrPac
   constexpr int TG = 4;  // tokens whose update loads are issued together
   const int lane = threadIdx.x;
   const int e0 = __builtin_amdgcn_readfirstlane(threadIdx.y) * C16_EPL;
-  const int blk = logical_block<false>(), slice = blk % nslices, chunk = blk / nslices;
+  const int blk = logical_block<false>();
+  int slice, chunk;
+  slice_chunk(blk, nslices, slice, chunk);
   const int cs = slice * C16_LANES, c = cs + lane;
   const bool cok = c < g.C;
   const T* ze[C16_EPL];
@@ -1626,7 +1656,9 @@ __global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgradz(const bf16_t* __
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.y);
   const int nw = blockDim.y, nthr = C16_LANES * nw, tid = wave * C16_LANES + lane;
   const int e0 = wave * EPL;
-  const int blk = logical_block<false>(), slice = blk % nslices, chunk = blk / nslices;
+  const int blk = logical_block<false>();
+  int slice, chunk;
+  slice_chunk_unless8(blk, nslices, slice, chunk);
   const int cs = slice * C16_LANES, c = cs + lane;
   const bool cok = c < g.C;
   // this lane's update row slot: token zt_t, vector zt_j of the 64-channel row
@@ -1741,7 +1773,9 @@ __global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgradz_d2(const bf16_t*
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.y);
   const int nw = blockDim.y, nthr = C16_LANES * nw, tid = wave * C16_LANES + lane;
   const int e0 = wave * EPL;
-  const int blk = logical_block<false>(), slice = blk % nslices, chunk = blk / nslices;
+  const int blk = logical_block<false>();
+  int slice, chunk;
+  slice_chunk(blk, nslices, slice, chunk);
   const int cs = slice * C16_LANES, c = cs + lane;
   const bool cok = c < g.C;
   // this lane's update staging slot: lane half h (events k = h, h + 2, ... of the wave's
@@ -1995,7 +2029,9 @@ __global__ void __launch_bounds__(256) k_triangular(const T* __restrict__ base, 
   extern __shared__ float lds[];
   const int BCG = blockDim.x, TL = blockDim.y;
   const int BC = BCG * V;
-  const int blk = logical_block<false>(), slice = blk % nslices, chunk = blk / nslices;
+  const int blk = logical_block<false>();
+  int slice, chunk;
+  slice_chunk(blk, nslices, slice, chunk);
   const int cs = slice * BC;
   const int A4 = (A + 3) & ~3;
   const int tid = threadIdx.y * BCG + threadIdx.x;
@@ -2078,7 +2114,9 @@ __global__ void __launch_bounds__(SIHC_EV_FWD_THREADS, SIHC_EV_MINW) k_event_fwd
   constexpr int S = K * K;
   constexpr int U = SIHC_EV_UNROLL;  // tokens per lane per iteration
   const int BCG = blockDim.x, TL = blockDim.y;
-  const int blk = logical_block<K == 4>(), slice = blk % nslices, chunk = blk / nslices;
+  const int blk = logical_block<K == 4>();
+  int slice, chunk;
+  slice_chunk(blk, nslices, slice, chunk);
   const int c0 = (slice * BCG + threadIdx.x) * V;
   if (c0 >= g.C) return;
   float bw[S][V], aw[S][V];
@@ -2272,7 +2310,9 @@ __global__ void __launch_bounds__(256, SIHC_EV_MINW) k_event_bwd(const T* __rest
   if (run_carry<T>(carry, S, g.C, red)) return;
   const int BCG = blockDim.x, TL = blockDim.y;
   const int BC = BCG * V;
-  const int blk = logical_block_of<K == 4>(carry.nmain), slice = blk % nslices, chunk = blk / nslices;
+  const int blk = logical_block_of<K == 4>(carry.nmain);
+  int slice, chunk;
+  slice_chunk(blk, nslices, slice, chunk);
   const int c0 = slice * BC + threadIdx.x * V;
   float db[S][V], da[S][V];
 #pragma unroll
