@@ -819,31 +819,53 @@ def kernels(args) -> None:
     h = r((B, edge, edge, C), 0.0, 1e-2)
     cases.append(("event_backward", (3 * S + 3) * U,
                   lambda: launch.event_backward(h, ws[1], x, ws[0], beta[0], alpha[1])))
-    # reference rows: the calibration stream over the per-event kernels' own arrays (one
-    # 4-slot carrier-shaped array is 4 workspace-shaped ones; U bytes each)
-    from sihc_hip import _lib
-
-    Lk = _lib.lib()
-    stv = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    carriers = [torch.empty(4 * U, dtype=torch.uint8, device=dev) for _ in range(3)]
-    wss = [torch.empty(U, dtype=torch.uint8, device=dev) for _ in range(4)]
-    arr = lambda ts: (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])  # noqa: E731
-    f_src, f_dst = arr([carriers[0], wss[0]]), arr([carriers[1], wss[1]])
-    b_src, b_dst = arr([carriers[0], carriers[1], wss[0], wss[1]]), arr([carriers[2], wss[2]])
-    if S == 4:
-        cases.append(("stream, the per-event forward's arrays (reference)", 10 * U,
-                      lambda: _lib.check(Lk.sihc_stream(f_src, 2, f_dst, 2, U, 1, stv))))
-        cases.append(("stream, the per-event backward's arrays (reference)", 15 * U,
-                      lambda: _lib.check(Lk.sihc_stream(b_src, 4, b_dst, 2, U, 2, stv))))
     xb = x[: B // 2].contiguous()
     idx = group_index(B // 2, 16, 5, seed=3).to(dev)
     cells = launch.gather_cells(xb, idx, S)
     cases.append(("gather_cells (config 3)", 2 * S * U // 2, lambda: launch.gather_cells(xb, idx, S)))
     cases.append(("scatter_cells (config 3)", 2 * S * U // 2, lambda: launch.scatter_cells(cells, idx)))
+    # Reference point of each op: the one-shot calibration stream over the op's own arrays
+    # (sihc_stream_mix: carrier-shaped sources, workspace-shaped sources, carrier-shaped
+    # destinations, workspace-shaped destinations), the same bytes as the op moves.
+    mixes = {"event_forward": (1, 1, 1, 1), "event_backward": (2, 2, 1, 1),
+             "write_impl (add_x=False) E=24": (0, 24, 1, 0),
+             "gather_cells (config 3)": (1, 0, 1, 0), "scatter_cells (config 3)": (1, 0, 1, 0)}
+    for e in (1, 16, 24):
+        mixes[f"read E={e}"] = (1, 0, 0, e)
+        mixes[f"write E={e}"] = (1, e, 1, 0)
+        mixes[f"weight_grad E={e}"] = (1, e, 0, 0)
+    for a in (1, 11, 12, 23):
+        mixes[f"triangular A={a}"] = (0, a + 1, 0, 1)
+        mixes[f"triangular_gamma_grad A={a}"] = (0, a + 1, 0, 0)
+        mixes[f"triangular_backward A={a}"] = (0, a + 1, 0, a)
+    from sihc_hip import _lib
+
+    Lk = _lib.lib()
+    stv = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    car_src = [torch.empty(S * U, dtype=torch.uint8, device=dev) for _ in range(2)]
+    car_dst = torch.empty(S * U, dtype=torch.uint8, device=dev)
+    ws_dst = [torch.empty(U, dtype=torch.uint8, device=dev) for _ in range(24)]
+    sink = torch.empty(U // 64, dtype=torch.uint8, device=dev)
+    arr = lambda ts: (ctypes.c_void_p * max(1, len(ts)))(*[t.data_ptr() for t in ts])  # noqa: E731
+
+    def stream_of(name):
+        ncs, nws, ncd, nwd = mixes[name]
+        half = name.endswith("(config 3)")  # gather / scatter run at half the batch
+        srcs = arr(car_src[:ncs] + ws[:nws])
+        dsts = arr(([car_dst] if ncd else []) + ws_dst[:nwd])
+        nb = U // 2 if half else U
+        return lambda: _lib.check(Lk.sihc_stream_mix(srcs, ncs + nws, ncs, dsts, ncd + nwd, ncd, S, nb,
+                                                     ctypes.c_void_p(sink.data_ptr()), stv))
+
     for name, nbytes, fn in cases:
         t = timed(fn)
-        print(json.dumps({"kernel": name, "us": round(t * 1e6, 1), "bytes": nbytes,
-                          "GB/s": round(nbytes / t / 1e9, 1), "frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}),
+        row = {"kernel": name, "us": round(t * 1e6, 1), "bytes": nbytes,
+               "GB/s": round(nbytes / t / 1e9, 1), "frac": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)}
+        if name in mixes:
+            ts = timed(stream_of(name))
+            row["stream_us"] = round(ts * 1e6, 1)
+            row["of_stream"] = round(ts / t, 4)
+        print(json.dumps(row),
               flush=True)
 
 

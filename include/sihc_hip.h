@@ -252,6 +252,18 @@ int sihc_scatter_add_cells(const void *cells, const int32_t *index, void *x, int
 int sihc_stream(const void *const *src, int nsrc, void *const *dst, int ndst, size_t bytes,
                 int shape, void *stream);
 
+/* The same one-shot stream over any op's own array mix, the reference point each stage op
+ * is read against: nsrc sources and ndst destinations (0..SIHC_MAX_EVENTS each, not both
+ * 0), of which the first ncar_src / ncar_dst are carrier-shaped (slots x `bytes`: slots 1,
+ * 4 or 16) and the rest workspace-shaped (`bytes`, a multiple of 4096). Destination w gets
+ * the XOR of the thread's source vectors ^ (w * slots + q) for slot unit q of a
+ * carrier-shaped one, ^ w otherwise. A read-only mix (ndst = 0) stores one 16-byte XOR per
+ * wave into `sink`, which must hold bytes / 64 bytes (ignored otherwise). The library cannot
+ * see array sizes: carrier-shaped arrays MUST hold slots x `bytes` bytes.
+ * No reference counterpart: the HBM reference point of the stage ops (bench.py --mode kernels). */
+int sihc_stream_mix(const void *const *src, int nsrc, int ncar_src, void *const *dst, int ndst,
+                    int ncar_dst, int slots, size_t bytes, void *sink, void *stream);
+
 /* Plain device copy of `bytes` bytes (16-byte vectors). No reference counterpart: it is
  * the calibration kernel for HBM counters and the practical bandwidth ceiling. */
 int sihc_copy(const void *src, void *dst, size_t bytes, void *stream);

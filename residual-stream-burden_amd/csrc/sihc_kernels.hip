@@ -2720,6 +2720,53 @@ __global__ void __launch_bounds__(256) k_stream(PtrPack src, PtrPack dst, int64_
   }
 }
 
+// The same one-shot stream over any op's own array mix: sources and destinations in any
+// number up to 32, the first ncs sources and the first ncd destinations carrier-shaped
+// (`slots` 4 KB units of each per block: a cell's slots), the others workspace-shaped (one
+// unit). Loads go out eight at a time before they are combined. Destination w gets the
+// XOR of every source vector of the thread ^ (w * slots + q) for slot q of a carrier-shaped
+// one, ^ w otherwise. With no destination (a read-only mix, as a weight gradient's) each
+// wave stores the XOR of its lanes' values to sink[u * 4 + wave], 1/256 of the bytes read.
+__global__ void __launch_bounds__(256) k_stream_mix(PtrPack src, int nsrc, int ncs, PtrPack dst, int ndst, int ncd,
+                                                    int slots, int64_t units, u32x4* __restrict__ sink) {
+  const int64_t u = blockIdx.x;
+  if (u >= units) return;
+  const int t = int(threadIdx.x);
+  u32x4 acc = {uint32_t(u), uint32_t(t), 0u, 0u};
+  const int ncv = ncs * slots;           // carrier source vectors
+  const int nv = ncv + (nsrc - ncs);     // all source vectors of the thread
+  for (int i0 = 0; i0 < nv; i0 += 8) {   // i0 is uniform: the source and slot are scalars
+    u32x4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int i = min(i0 + k, nv - 1);  // past the end: the last vector again, not combined
+      const bool car = i < ncv;
+      const int r = car ? i / slots : ncs + (i - ncv);
+      const int64_t off = car ? (u * slots + (i - (i / slots) * slots)) * 256 + t : u * 256 + t;
+      v[k] = ld<true>(static_cast<const u32x4*>(src.p[r]) + off);
+    }
+    load_fence();
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (i0 + k < nv) acc ^= v[k];
+  }
+  for (int w = 0; w < ndst; ++w) {
+    u32x4* b = static_cast<u32x4*>(const_cast<void*>(dst.p[w]));
+    if (w < ncd) {
+      for (int q = 0; q < slots; ++q) st<true>(b + (u * slots + q) * 256 + t, acc ^ uint32_t(w * slots + q));
+    } else {
+      st<true>(b + u * 256 + t, acc ^ uint32_t(w));
+    }
+  }
+  if (ndst == 0) {
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[k] ^= uint32_t(__shfl_xor(int(acc[k]), m, 64));
+    if (t % 64 == 0) sink[u * 4 + t / 64] = acc;
+  }
+}
+
 __global__ void k_copy1(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t n) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) dst[i] = src[i];
@@ -4127,6 +4174,35 @@ int sihc_stream(const void* const* src, int nsrc, void* const* dst, int ndst, si
   if (nsrc == 2 && ndst == 2) return go(k_stream<2, 2, 0, 0>);
   if (nsrc == 4 && ndst == 2) return go(k_stream<4, 2, 0, 0>);
   return go(k_stream<0, 1, 0, 0>);
+}
+
+int sihc_stream_mix(const void* const* src, int nsrc, int ncar_src, void* const* dst, int ndst, int ncar_dst,
+                    int slots, size_t bytes, void* sink, void* stream) {
+  const char* what = "sihc_stream_mix";
+  if (bytes == 0) return SIHC_OK;
+  if (nsrc < 0 || nsrc > SIHC_MAX_EVENTS || ndst < 0 || ndst > SIHC_MAX_EVENTS || nsrc + ndst == 0)
+    return fail(SIHC_ERR_INVALID, "%s: %d sources and %d destinations (0..%d each, not both 0)", what, nsrc, ndst,
+                SIHC_MAX_EVENTS);
+  if (ncar_src < 0 || ncar_src > nsrc || ncar_dst < 0 || ncar_dst > ndst)
+    return fail(SIHC_ERR_INVALID, "%s: carrier-shaped counts %d / %d exceed the array counts", what, ncar_src,
+                ncar_dst);
+  if (slots != 1 && slots != 4 && slots != 16) return fail(SIHC_ERR_INVALID, "%s: slots must be 1, 4 or 16", what);
+  if (bytes % 4096) return fail(SIHC_ERR_INVALID, "%s: bytes must be a multiple of 4096", what);
+  if ((nsrc > 0 && !src) || (ndst > 0 && !dst)) return fail(SIHC_ERR_INVALID, "%s: null array", what);
+  for (int i = 0; i < nsrc; ++i)
+    if (!src[i] || !aligned(src[i], 16)) return fail(SIHC_ERR_INVALID, "%s: source %d null or misaligned", what, i);
+  for (int i = 0; i < ndst; ++i)
+    if (!dst[i] || !aligned(dst[i], 16)) return fail(SIHC_ERR_INVALID, "%s: destination %d null or misaligned", what, i);
+  if (ndst == 0 && (!sink || !aligned(sink, 16)))
+    return fail(SIHC_ERR_INVALID, "%s: a read-only mix needs a 16-byte aligned sink", what);
+  const int64_t units = int64_t(bytes / 4096);
+  if (units > 0x7fffffff) return fail(SIHC_ERR_INVALID, "%s: too many units", what);
+  PtrPack ps{}, pd{};
+  for (int i = 0; i < nsrc; ++i) ps.p[i] = src[i];
+  for (int i = 0; i < ndst; ++i) pd.p[i] = dst[i];
+  hipLaunchKernelGGL(k_stream_mix, dim3(unsigned(units)), dim3(256), 0, static_cast<hipStream_t>(stream), ps, nsrc,
+                     ncar_src, pd, ndst, ncar_dst, slots, units, static_cast<u32x4*>(ndst == 0 ? sink : nullptr));
+  return check_launch(what);
 }
 
 int sihc_copy(const void* src, void* dst, size_t bytes, void* stream) {

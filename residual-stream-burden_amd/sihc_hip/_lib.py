@@ -53,6 +53,7 @@ PROTOTYPES: dict[str, tuple] = {
     "sihc_scatter_cells": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
     "sihc_scatter_add_cells": (_i32, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i32, _vp]),
     "sihc_stream": (_i32, [_vpp, _i32, _vpp, _i32, _sz, _i32, _vp]),
+    "sihc_stream_mix": (_i32, [_vpp, _i32, _i32, _vpp, _i32, _i32, _i32, _sz, _vp, _vp]),
     "sihc_copy": (_i32, [_vp, _vp, _sz, _vp]),
 }
 

@@ -169,6 +169,28 @@ def test_stream_calibration_arguments_are_validated():
     assert b"shape 2 takes" in lib.sihc_last_error()
 
 
+def test_stream_mix_arguments_are_validated():
+    lib = _lib.lib()
+    arr = _lib.ptr_array([FAKE] * 33)
+    assert lib.sihc_stream_mix(arr, 33, 0, arr, 1, 0, 1, 1 << 20, None, None) == 1
+    assert b"sources and" in lib.sihc_last_error()
+    assert lib.sihc_stream_mix(arr, 0, 0, arr, 0, 0, 1, 1 << 20, None, None) == 1
+    assert b"not both 0" in lib.sihc_last_error()
+    assert lib.sihc_stream_mix(arr, 2, 3, arr, 1, 0, 4, 1 << 20, None, None) == 1
+    assert b"carrier-shaped counts" in lib.sihc_last_error()
+    assert lib.sihc_stream_mix(arr, 2, 1, arr, 1, 2, 4, 1 << 20, None, None) == 1
+    assert b"carrier-shaped counts" in lib.sihc_last_error()
+    assert lib.sihc_stream_mix(arr, 2, 1, arr, 1, 0, 8, 1 << 20, None, None) == 1
+    assert b"slots must be" in lib.sihc_last_error()
+    assert lib.sihc_stream_mix(arr, 2, 1, arr, 1, 0, 4, 1000, None, None) == 1
+    assert b"multiple of 4096" in lib.sihc_last_error()
+    assert lib.sihc_stream_mix(_lib.ptr_array([FAKE, FAKE + 8]), 2, 1, arr, 1, 0, 4, 1 << 20, None, None) == 1
+    assert b"misaligned" in lib.sihc_last_error()
+    assert lib.sihc_stream_mix(arr, 2, 1, arr, 0, 0, 4, 1 << 20, None, None) == 1
+    assert b"needs a 16-byte aligned sink" in lib.sihc_last_error()
+    assert lib.sihc_stream_mix(arr, 2, 1, arr, 0, 0, 4, 0, None, None) == 0  # nothing to move
+
+
 def test_oversized_tensor_is_rejected():
     lib = _lib.lib()
     outs = _lib.ptr_array([FAKE])

@@ -158,3 +158,60 @@ def test_stream_calibration_kernel(nr, nw, shape):
                 assert torch.equal(d.view(units, 4, 256, 4)[:, q], acc ^ (4 * j + q)), f"output {j} slot {q}"
         else:
             assert torch.equal(d.view(units, 256, 4), acc ^ j), f"output {j}"
+
+
+# (sources, carrier-shaped sources, destinations, carrier-shaped destinations, slots): the
+# mixes of a 16-slot read and write, a read-only weight gradient (sink), the triangular op
+# and its fused backward, a write-only mix, and 9-17 vectors (two and three load batches)
+MIX_CASES = [(1, 1, 5, 0, 16), (3, 1, 1, 1, 16), (9, 1, 0, 0, 4), (13, 0, 1, 0, 1), (12, 0, 11, 0, 1),
+             (0, 0, 2, 1, 4), (2, 2, 3, 2, 4), (32, 0, 32, 0, 1)]
+
+
+@pytest.mark.parametrize("ns,ncs,nd,ncd,slots", MIX_CASES,
+                         ids=[f"{a}c{b}-{c}c{d}-s{e}" for a, b, c, d, e in MIX_CASES])
+def test_stream_mix_kernel(ns, ncs, nd, ncd, slots):
+    # sihc_stream_mix: unit u, thread t: acc = {u, t, 0, 0} XOR every source vector of the
+    # thread (vector u*256 + t of a workspace-shaped source, (u*slots + q)*256 + t of a
+    # carrier-shaped one); destination w gets acc ^ (w*slots + q) (carrier-shaped) or acc ^ w;
+    # with no destination each wave's XOR over its 64 lanes lands in sink[u*4 + wave].
+    import ctypes
+
+    from sihc_hip import _lib
+
+    announce(f"stream mix {ns}({ncs}):{nd}({ncd}) slots {slots}")
+    L = _lib.lib()
+    units = 37
+    n = 4096 * units
+    g = torch.Generator(device="cuda").manual_seed(ns * 100 + nd * 10 + slots)
+    rint = lambda m: torch.randint(0, 2 ** 31 - 1, (m * n // 4,), device="cuda", generator=g, dtype=torch.int32)  # noqa
+    srcs = [rint(slots if r < ncs else 1) for r in range(ns)]
+    dsts = [torch.zeros((slots if w < ncd else 1) * n // 4, device="cuda", dtype=torch.int32) for w in range(nd)]
+    sink = torch.zeros(units * 4 * 4, device="cuda", dtype=torch.int32)
+    sp = (ctypes.c_void_p * max(ns, 1))(*[t.data_ptr() for t in srcs])
+    dp = (ctypes.c_void_p * max(nd, 1))(*[t.data_ptr() for t in dsts])
+    _lib.check(L.sihc_stream_mix(sp, ns, ncs, dp, nd, ncd, slots, n, ctypes.c_void_p(sink.data_ptr()),
+                                 ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    torch.cuda.synchronize()
+    acc = torch.zeros(units, 256, 4, device="cuda", dtype=torch.int32)
+    acc[:, :, 0] = torch.arange(units, device="cuda", dtype=torch.int32)[:, None]
+    acc[:, :, 1] = torch.arange(256, device="cuda", dtype=torch.int32)[None, :]
+    for r, t in enumerate(srcs):
+        if r < ncs:
+            for q in range(slots):
+                acc ^= t.view(units, slots, 256, 4)[:, q]
+        else:
+            acc ^= t.view(units, 256, 4)
+    for w, d in enumerate(dsts):
+        if w < ncd:
+            for q in range(slots):
+                assert torch.equal(d.view(units, slots, 256, 4)[:, q], acc ^ (w * slots + q)), f"output {w} slot {q}"
+        else:
+            assert torch.equal(d.view(units, 256, 4), acc ^ w), f"output {w}"
+    if nd == 0:
+        waves = acc.view(units, 4, 64, 4)
+        red = waves[:, :, 0]
+        for lane in range(1, 64):
+            red = red ^ waves[:, :, lane]
+        assert torch.equal(sink.view(units, 4, 4), red), "sink"
+    else:
+        assert not sink.any(), "the sink is written only by read-only mixes"
