@@ -1885,6 +1885,86 @@ __global__ void __launch_bounds__(512, SIHC_C16Z_MINW) k_wgradz_d2(const bf16_t*
 }
 
 // ----------------------------------------------------------------------------------
+// γ gradient partials on 16-byte row lanes (bf16, 3..32 updates, C % 8 == 0, 16-byte
+// aligned rows): part[chunk][j][c] = sum over the chunk's tokens m of g[m,c] * u_j[m,c].
+// A read-only mix of 1 + A workspace rows. A block is 16 lanes of 8 channels (a 128-channel
+// slice) x G update groups x 16 / G token rows (256 threads). Group y takes updates
+// y*NA .. y*NA + NA - 1 (past A: the last update again, never written). Every thread
+// streams the chunk's tokens r, r + 16 / G, ...: the gradient vector and its NA update
+// vectors with 16-byte non-temporal loads, all issued before they are used, summed in fp32
+// registers. Nothing is staged in LDS on the way, and there is no barrier in the loop:
+// against the LDS-tile kernels (an 8-token tile through registers and LDS, two barriers
+// a tile) this ran A = 9 262 -> 229 us, A = 12 324 -> 296, A = 17 453 -> 407, A = 24
+// 613 -> 577 at 65,536 rows x 1152 channels. The group's token rows are then summed in
+// ascending row order through LDS, one update at a time; each chunk's sum has a fixed
+// order, so the result is bitwise repeatable.
+// ----------------------------------------------------------------------------------
+template <int NA>
+__global__ void __launch_bounds__(256) k_gamma_rows(const bf16_t* __restrict__ grad, PtrPack z,
+                                                    float* __restrict__ part, int A, int M, int C, int tpb,
+                                                    int nslices) {
+  __shared__ float red[256 * 8];  // [token row][group][lane][8]
+  const int lx = int(threadIdx.x), gy = int(threadIdx.y), r = int(threadIdx.z);
+  const int G = int(blockDim.y), TR = int(blockDim.z);
+  int slice, chunk;
+  slice_chunk(int(blockIdx.x), nslices, slice, chunk);
+  const int c0 = slice * 128 + lx * 8;
+  const int j0 = gy * NA;
+  float acc[NA][8];
+#pragma unroll
+  for (int q = 0; q < NA; ++q)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[q][k] = 0.f;
+  if (c0 < C) {
+    const int m_end = min(chunk * tpb + tpb, M);
+    const u32x4* up[NA];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) up[q] = static_cast<const u32x4*>(z.p[min(j0 + q, A - 1)]);
+    const u32x4* gp = reinterpret_cast<const u32x4*>(grad);
+    for (int m = chunk * tpb + r; m < m_end; m += TR) {
+      const int64_t o = (int64_t(m) * C + c0) >> 3;  // 16-byte vector index
+      const u32x4 gv = ld<true>(gp + o);
+      u32x4 uv[NA];
+#pragma unroll
+      for (int q = 0; q < NA; ++q) uv[q] = ld<true>(up[q] + o);
+      load_fence();
+      // the gradient's 8 values first, then update by update (this order sets the register
+      // allocation, and with it the occupancy the group table was measured at: 4 waves per
+      // SIMD for 6-8 updates per lane; interleaved per word, 6 took 96 VGPRs and 5 waves, and
+      // A = 23 ran 557 -> 587 us)
+      float gf[8];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        gf[2 * k] = __uint_as_float(gv[k] << 16);
+        gf[2 * k + 1] = __uint_as_float(gv[k] & 0xffff0000u);
+      }
+#pragma unroll
+      for (int q = 0; q < NA; ++q)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          acc[q][2 * k] = fmaf(gf[2 * k], __uint_as_float(uv[q][k] << 16), acc[q][2 * k]);
+          acc[q][2 * k + 1] = fmaf(gf[2 * k + 1], __uint_as_float(uv[q][k] & 0xffff0000u), acc[q][2 * k + 1]);
+        }
+    }
+  }
+  const int tid = (r * G + gy) * 16 + lx;
+#pragma unroll
+  for (int q = 0; q < NA; ++q) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) red[tid * 8 + k] = acc[q][k];
+    __syncthreads();
+    for (int i = tid; i < G * 128; i += 256) {  // (group, channel of the slice)
+      const int gi = i >> 7, cl = i & 127;
+      float sum = 0.f;
+      for (int rr = 0; rr < TR; ++rr) sum += red[(rr * G + gi) * 128 + cl];
+      const int j = gi * NA + q, c = slice * 128 + cl;
+      if (j < A && c < C) part[(int64_t(chunk) * A + j) * C + c] = sum;
+    }
+    __syncthreads();
+  }
+}
+
+// ----------------------------------------------------------------------------------
 // Fixed-order sum of partial rows. part is [chunks][R][S][C]; row r of the result
 // goes to out0 + r*C*S ([R][C][S], `pair` == 0) or, with `pair`, row 0 -> out0 and
 // row 1 -> out1 (each [C][S]). Rows whose bit is set in zero_mask are written as
@@ -3307,18 +3387,37 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
             else if (events <= 18) goz(IC<2>{}, IC<1>{}, IC<3>{}, (events + 2) / 3);
             else if (events <= 24) goz(IC<2>{}, IC<1>{}, IC<6>{}, 4);
             else goz(IC<2>{}, IC<1>{}, IC<4>{}, (events + 3) / 4);
-          } else if (!CAR && !SD && bf && events >= 2 && events <= 16) {
-            // gamma gradient (one-slot workspace rows, 64-vector tile: one per thread of a
-            // wave) on the pipelined kernel, shapes measured per update count at 65,536 rows x
-            // 1152 channels: A = 3 1 x 3 105 us (LDS-tile kernel: 150), A = 5 1 x 6 150 (187),
-            // A = 8 4 x 2 218 (247), A = 10 2 x 6 275 (305); past 16 the LDS-tile kernel is as fast
-            if (events == 2) goz(IC<1>{}, IC<1>{}, IC<2>{}, 1);
-            else if (events == 3) goz(IC<1>{}, IC<1>{}, IC<3>{}, 1);
-            else if (events == 4) goz(IC<1>{}, IC<1>{}, IC<4>{}, 1);
-            else if (events <= 6) goz(IC<1>{}, IC<1>{}, IC<6>{}, 1);
-            else if (events <= 8) goz(IC<1>{}, IC<1>{}, IC<2>{}, 4);
-            else if (events <= 12) goz(IC<1>{}, IC<1>{}, IC<6>{}, 2);
-            else goz(IC<1>{}, IC<1>{}, IC<8>{}, 2);
+          } else if (!CAR && !SD && bf && events == 2) {
+            // gamma gradient of 2 updates: the pipelined kernel on one-slot rows (1 wave x 2
+            // updates: 77 us at 65,536 rows x 1152 channels; row lanes 81)
+            goz(IC<1>{}, IC<1>{}, IC<2>{}, 1);
+          } else if (!CAR && !SD && bf && events >= 3) {
+            // gamma gradient of 3..32 updates on row lanes (k_gamma_rows), update groups per
+            // block measured per update count at 65,536 rows x 1152 channels: A = 3-4 in 4
+            // groups (A = 4 124 -> 117 us), 5-10 in one (A = 9 262 -> 229), 11-22 in two (A =
+            // 17 453 -> 407), 23-32 in four (A = 32 798 -> 767); against the previous kernels
+            const int G = events <= 4 ? 4 : events <= 10 ? 1 : events <= 22 ? 2 : 4;
+            const int slr = (g.C + 127) / 128;
+            auto gorows = [&](auto na) {
+              constexpr int NA = decltype(na)::value;
+              chunks = whole_rounds(slr, max_chunks,
+                                    resident_blocks(reinterpret_cast<const void*>(&k_gamma_rows<NA>), 256, 0));
+              const int tpr = int((int64_t(g.M) + chunks - 1) / chunks);
+              if (tpr > 0) chunks = int((int64_t(g.M) + tpr - 1) / tpr);  // no chunk past the last token
+              hipLaunchKernelGGL((k_gamma_rows<NA>), dim3(blocks1d(slr, chunks)), dim3(16, G, 16 / G), 0, st,
+                                 reinterpret_cast<const bf16_t*>(x), pk, part, events, int(g.M), g.C, tpr, slr);
+            };
+            switch ((events + G - 1) / G) {
+              case 1: gorows(IC<1>{}); break;
+              case 5: gorows(IC<5>{}); break;
+              case 6: gorows(IC<6>{}); break;
+              case 7: gorows(IC<7>{}); break;
+              case 8: gorows(IC<8>{}); break;
+              case 9: gorows(IC<9>{}); break;
+              case 10: gorows(IC<10>{}); break;
+              case 11: gorows(IC<11>{}); break;
+              default: return fail(SIHC_ERR_INVALID, "%s: internal gamma-gradient shape", what);
+            }
           } else {
             if (events <= 2) {
               // fused triangular backward: 1 update hints loads only, 2 updates stores

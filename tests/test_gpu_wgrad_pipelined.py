@@ -7,7 +7,9 @@ the other kernels.
 Products of bf16 values are exact in fp32 and the sums are fp32, so the fp32 bar applies
 against the oracle's float64 sums of the same bf16 inputs. Token tails (grids of 5x5
 cells), channel tails (136 = 2 x 64 + 8 channels; 24 channels in one 64-lane slice) and
-per-batch state permutations are covered.
+per-batch state permutations are covered. The gamma gradient (one-slot workspace rows)
+runs on the pipelined kernel for 2 updates and on 16-byte row lanes for 3..32 (136
+channels: a second 128-channel slice holding one lane; 24: three lanes of one slice).
 """
 from __future__ import annotations
 
@@ -76,7 +78,10 @@ def test_carrier_weight_grad_bf16(slots, events, geom):
     assert torch.equal(got, launch.weight_grad(x, ups, w, index=idx, out_dtype=torch.float32))
 
 
-GAMMA_CASES = [2, 3, 4, 5, 6, 7, 8, 9, 12, 13, 16, 17]  # waves x updates per lane: 1 x A ... 2 x 8; 17: LDS tile
+# 2: the pipelined kernel (1 wave x 2 updates); 3..32: row lanes, update groups x updates per
+# lane 4 x 1 (3, 4: the last group repeats an update), 1 x A (5..10), 2 x 6..11 (11..22, odd
+# counts half-filled), 4 x 6..8 (23..32)
+GAMMA_CASES = [2, 3, 4, 5, 7, 10, 11, 12, 17, 22, 23, 25, 32]
 
 
 @pytest.mark.parametrize("active", GAMMA_CASES)
@@ -84,7 +89,7 @@ GAMMA_CASES = [2, 3, 4, 5, 6, 7, 8, 9, 12, 13, 16, 17]  # waves x updates per la
                          ids=["r507-c136", "r4096-c1152", "r77-c24"])
 def test_gamma_grad_bf16(active, rows, channels):
     # the gamma gradient of the triangular op over bf16 workspace rows: sum over rows of
-    # grad * update_j, one slot per row, on the same pipelined kernel (2..16 updates)
+    # grad * update_j (the pipelined kernel for 2 updates, row lanes for 3..32)
     announce(f"gamma grad bf16 A={active} rows={rows} C={channels}")
     torch.manual_seed(5 * active + channels)
     grad = torch.randn(1, rows, channels, device="cuda").to(torch.bfloat16)
