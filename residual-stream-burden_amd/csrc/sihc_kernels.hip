@@ -1965,6 +1965,92 @@ __global__ void __launch_bounds__(256) k_gamma_rows(const bf16_t* __restrict__ g
 }
 
 // ----------------------------------------------------------------------------------
+// 4-slot carrier weight-gradient partials on the same row lanes (bf16, 16-byte rows):
+// part[chunk][e][s][c] = sum over the chunk's tokens m of x[m,s,c] * z_e[m,c]. Lane = 8
+// channels of a 128-channel slice; update group y takes events y*NA .. y*NA + NA - 1 (past
+// E: the last event again, never written); each thread streams the chunk's tokens r,
+// r + 16 / G, ...: the cell's 4 slot vectors (through the state index if any) and its NA
+// update vectors, 4 x 8 x NA fp32 sums in registers. Every group loads the cell's slot
+// vectors (the other groups' copies come from L2); nothing is staged in LDS. Measured per
+// event count against the pipelined kernel at the XL shape (batch 256, D = 1152): E = 5
+// 280 -> 249 us, E = 12 414 -> 372, E = 16 525 -> 501, E = 24 734 -> 712, E = 32 1067 ->
+// 923; E = 3-4 and 17-18 keep the pipelined kernel (as fast there, or faster).
+// ----------------------------------------------------------------------------------
+template <int NA>
+__global__ void __launch_bounds__(256) k_wgrad_rows(const bf16_t* __restrict__ x, PtrPack z, float* __restrict__ part,
+                                                    const int32_t* __restrict__ index, int E, Geo g, int tpb,
+                                                    int nslices) {
+  constexpr int S = 4;
+  __shared__ float red[256 * 8];  // [token row][group][lane][8]
+  const int lx = int(threadIdx.x), gy = int(threadIdx.y), r = int(threadIdx.z);
+  const int G = int(blockDim.y), TR = int(blockDim.z);
+  int slice, chunk;
+  slice_chunk(int(blockIdx.x), nslices, slice, chunk);
+  const int c0 = slice * 128 + lx * 8;
+  const int j0 = gy * NA;
+  float acc[NA][S][8];
+#pragma unroll
+  for (int q = 0; q < NA; ++q)
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) acc[q][s][k] = 0.f;
+  if (c0 < g.C) {
+    const int m_end = min(chunk * tpb + tpb, g.M);
+    const u32x4* up[NA];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) up[q] = static_cast<const u32x4*>(z.p[min(j0 + q, E - 1)]);
+    for (int m = chunk * tpb + r; m < m_end; m += TR) {
+      const int64_t p0 = cell_pixel0(m, g, index);
+      u32x4 xv[S];
+#pragma unroll
+      for (int s = 0; s < S; ++s) xv[s] = ld<true>(reinterpret_cast<const u32x4*>(x + slot_offset<2>(p0, s, g, c0)));
+      const int64_t o = (int64_t(m) * g.C + c0) >> 3;  // 16-byte vector index of the update rows
+      u32x4 uv[NA];
+#pragma unroll
+      for (int q = 0; q < NA; ++q) uv[q] = ld<true>(up[q] + o);
+      load_fence();
+      float xf[S][8];
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          xf[s][2 * k] = __uint_as_float(xv[s][k] << 16);
+          xf[s][2 * k + 1] = __uint_as_float(xv[s][k] & 0xffff0000u);
+        }
+#pragma unroll
+      for (int q = 0; q < NA; ++q)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float z0 = __uint_as_float(uv[q][k] << 16), z1 = __uint_as_float(uv[q][k] & 0xffff0000u);
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            acc[q][s][2 * k] = fmaf(xf[s][2 * k], z0, acc[q][s][2 * k]);
+            acc[q][s][2 * k + 1] = fmaf(xf[s][2 * k + 1], z1, acc[q][s][2 * k + 1]);
+          }
+        }
+    }
+  }
+  const int tid = (r * G + gy) * 16 + lx;
+#pragma unroll
+  for (int q = 0; q < NA; ++q)
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) red[tid * 8 + k] = acc[q][s][k];
+      __syncthreads();
+      for (int i = tid; i < G * 128; i += 256) {  // (group, channel of the slice)
+        const int gi = i >> 7, cl = i & 127;
+        float sum = 0.f;
+        for (int rr = 0; rr < TR; ++rr) sum += red[(rr * G + gi) * 128 + cl];
+        const int e = gi * NA + q, c = slice * 128 + cl;
+        if (e < E && c < g.C) part[((int64_t(chunk) * E + e) * S + s) * g.C + c] = sum;
+      }
+      __syncthreads();
+    }
+}
+
+// ----------------------------------------------------------------------------------
 // Fixed-order sum of partial rows. part is [chunks][R][S][C]; row r of the result
 // goes to out0 + r*C*S ([R][C][S], `pair` == 0) or, with `pair`, row 0 -> out0 and
 // row 1 -> out1 (each [C][S]). Rows whose bit is set in zero_mask are written as
@@ -3377,16 +3463,34 @@ int launch_wgrad(const char* what, const void* x, const void* const* z, void* ou
               hipLaunchKernelGGL((k_wgrad16<T>), dim3(blocks1d(slices16, chunks)), dim3(C16_LANES, nw), 0, st,
                                  static_cast<const T*>(x), pk, part, index, events, g, tpb, slices16, vs16);
             }
+          } else if (CAR && KK == 2 && bf && (events == 2 || (events >= 5 && events <= 16) ||
+                                               (events >= 19 && events <= 32))) {
+            // 4 slots on row lanes (k_wgrad_rows), update groups per block measured per event
+            // count at the XL shape: 2 for E = 2 and 5-6, 4 for 7-16, 8 for 19-32
+            const int G = events <= 6 ? 2 : events <= 16 ? 4 : 8;
+            const int slr = (g.C + 127) / 128;
+            auto gorows = [&](auto na) {
+              constexpr int NA = decltype(na)::value;
+              chunks = whole_rounds(slr, max_chunks,
+                                    resident_blocks(reinterpret_cast<const void*>(&k_wgrad_rows<NA>), 256, 0));
+              const int tpr = int((int64_t(g.M) + chunks - 1) / chunks);
+              if (tpr > 0) chunks = int((int64_t(g.M) + tpr - 1) / tpr);  // no chunk past the last token
+              hipLaunchKernelGGL((k_wgrad_rows<NA>), dim3(blocks1d(slr, chunks)), dim3(16, G, 16 / G), 0, st,
+                                 reinterpret_cast<const bf16_t*>(x), pk, part, index, events, g, tpr, slr);
+            };
+            switch ((events + G - 1) / G) {
+              case 1: gorows(IC<1>{}); break;
+              case 2: gorows(IC<2>{}); break;
+              case 3: gorows(IC<3>{}); break;
+              case 4: gorows(IC<4>{}); break;
+              default: return fail(SIHC_ERR_INVALID, "%s: internal weight-gradient shape", what);
+            }
           } else if (CAR && KK == 2 && bf && SIHC_WGZ_K2 && events >= 2) {
-            // 4 slots (one event keeps its direct kernel): E = 3 4 x 1 201 us (k_wgrad: 504),
-            // E = 9 3 x 3 355 us (k_wgrad: 622), E = 16 6 x 3 526 us (4 x 4: 573), E = 17-18
-            // 6 x 3 558-573 us (k_wgrad: 933-941), E = 28 7 x 4 923 us (k_wgrad: 1000)
-            if (events <= 4) goz(IC<2>{}, IC<1>{}, IC<1>{}, 4);           // idle waves only stage
-            else if (events <= 8) goz(IC<2>{}, IC<1>{}, IC<2>{}, 4);
-            else if (events == 9) goz(IC<2>{}, IC<2>{}, IC<3>{}, 3);
-            else if (events <= 18) goz(IC<2>{}, IC<1>{}, IC<3>{}, (events + 2) / 3);
-            else if (events <= 24) goz(IC<2>{}, IC<1>{}, IC<6>{}, 4);
-            else goz(IC<2>{}, IC<1>{}, IC<4>{}, (events + 3) / 4);
+            // 4 slots, 3-4 and 17-18 events (one event keeps its direct kernel): E = 3 4 x 1
+            // 201 us (k_wgrad: 504), E = 17-18 6 x 3 558-573 us (k_wgrad: 933-941; row lanes
+            // 579-592)
+            if (events <= 4) goz(IC<2>{}, IC<1>{}, IC<1>{}, 4);  // idle waves only stage
+            else goz(IC<2>{}, IC<1>{}, IC<3>{}, (events + 2) / 3);
           } else if (!CAR && !SD && bf && events == 2) {
             // gamma gradient of 2 updates: the pipelined kernel on one-slot rows (1 wave x 2
             // updates: 77 us at 65,536 rows x 1152 channels; row lanes 81)

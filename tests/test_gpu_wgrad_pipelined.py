@@ -1,9 +1,10 @@
 """GPU: the carrier weight gradient over every launch shape of its bf16 kernels.
 
 bf16 carriers with rows of whole 16-byte vectors and up to 32 events take the pipelined
-kernel (one channel per lane, EPL events per lane, 2..8 event waves chosen per event
-count); one event at 4 slots, channel counts that are not multiples of 8 and fp32 take
-the other kernels.
+kernels (one channel per lane, EPL events per lane, 2..8 event waves chosen per event
+count) or, at 4 slots for most event counts, 16-byte row lanes (8 channels x 4 slots x
+1-4 events per thread, 2, 4 or 8 event groups); one event at 4 slots, channel counts that
+are not multiples of 8 and fp32 take the other kernels.
 Products of bf16 values are exact in fp32 and the sums are fp32, so the fp32 bar applies
 against the oracle's float64 sums of the same bf16 inputs. Token tails (grids of 5x5
 cells), channel tails (136 = 2 x 64 + 8 channels; 24 channels in one 64-lane slice) and
@@ -22,22 +23,24 @@ from sihc_hip import launch
 
 pytestmark = pytest.mark.gpu
 
-CASES = [  # (slots, events): waves x events per lane of the pipelined kernel
+CASES = [  # (slots, events): the kernel and its shape
     (4, 1),    # the direct kernel
-    (4, 2),    # 4 x 1 (two waves stage only)
-    (4, 4),    # 4 x 1
-    (4, 5),    # 4 x 2 (last wave partly empty)
-    (4, 7),    # 4 x 2
-    (4, 8),    # 4 x 2
-    (4, 9),    # 3 x 3 (two vectors per thread)
-    (4, 12),   # 4 x 3
-    (4, 13),   # 5 x 3
-    (4, 16),   # 6 x 3
-    (4, 17),   # 6 x 3
-    (4, 20),   # 4 x 6
-    (4, 24),   # 4 x 6
-    (4, 25),   # 7 x 4
-    (4, 32),   # 8 x 4
+    (4, 2),    # row lanes, 2 groups x 1 event
+    (4, 3),    # pipelined 4 waves x 1 (one wave stages only)
+    (4, 4),    # pipelined 4 x 1
+    (4, 5),    # row lanes 2 x 3 (the last group repeats an event)
+    (4, 6),    # row lanes 2 x 3
+    (4, 7),    # row lanes 4 x 2 (one repeated event)
+    (4, 12),   # row lanes 4 x 3
+    (4, 13),   # row lanes 4 x 4 (three repeated)
+    (4, 16),   # row lanes 4 x 4
+    (4, 17),   # pipelined 6 waves x 3
+    (4, 18),   # pipelined 6 x 3
+    (4, 19),   # row lanes 8 x 3 (five repeated)
+    (4, 24),   # row lanes 8 x 3
+    (4, 25),   # row lanes 8 x 4
+    (4, 32),   # row lanes 8 x 4
+    # 16 slots: waves x events per lane of the pipelined dot2 kernel
     (16, 1),   # 4 x 1 (three waves stage only)
     (16, 4),   # 4 x 1
     (16, 5),   # 2 x 4
