@@ -3131,7 +3131,7 @@ int check_geometry(const char* what, int64_t batch, int grid, int cell, int chan
   if (cell != 2 && cell != 4) return fail(SIHC_ERR_INVALID, "%s: cell must be 2 or 4 (4 or 16 slots)", what);
   const int64_t M = batch * int64_t(grid) * grid;
   const int64_t carrier = M * cell * cell * int64_t(channels);
-  if (M >= (int64_t(1) << 31) || carrier >= (int64_t(1) << 47))
+  if (M >= SIHC_MAX_TOKENS || carrier >= (int64_t(1) << 47))
     return fail(SIHC_ERR_INVALID, "%s: tensor too large", what);
   g->M = int(M);
   g->GG = grid * grid;
@@ -3843,7 +3843,7 @@ int sihc_weight_grad(const void* x, const void* const* z, void* out, int events,
 int sihc_triangular(const void* base, const void* const* updates, const void* gamma, void* out, int active,
                     int64_t rows, int channels, int dtype, int gamma_dtype, void* stream) {
   const char* what = "sihc_triangular";
-  if (rows < 0 || rows >= (int64_t(1) << 31) || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
+  if (rows < 0 || rows >= SIHC_MAX_TOKENS || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
   if (!valid_dtype(dtype) || !valid_dtype(gamma_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
   if (int rc = check_count(what, active)) return rc;
   if (rows == 0) return SIHC_OK;  // empty tensors may carry NULL data pointers
@@ -3896,7 +3896,7 @@ int sihc_triangular_gamma_grad(const void* grad, const void* const* updates, voi
                                int channels, int dtype, int out_dtype, void* workspace, size_t workspace_bytes,
                                void* stream) {
   const char* what = "sihc_triangular_gamma_grad";
-  if (rows < 0 || rows >= (int64_t(1) << 31) || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
+  if (rows < 0 || rows >= SIHC_MAX_TOKENS || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
   if (!valid_dtype(dtype) || !valid_dtype(out_dtype)) return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
   if (int rc = check_count(what, active)) return rc;
   if (!out) return fail(SIHC_ERR_INVALID, "%s: null output", what);
@@ -3921,7 +3921,7 @@ int sihc_triangular_backward(const void* grad, const void* const* updates, const
                              int dtype, int gamma_dtype, int out_dtype, void* workspace, size_t workspace_bytes,
                              void* stream) {
   const char* what = "sihc_triangular_backward";
-  if (rows < 0 || rows >= (int64_t(1) << 31) || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
+  if (rows < 0 || rows >= SIHC_MAX_TOKENS || channels <= 0) return fail(SIHC_ERR_INVALID, "%s: bad sizes", what);
   if (!valid_dtype(dtype) || !valid_dtype(gamma_dtype) || !valid_dtype(out_dtype))
     return fail(SIHC_ERR_INVALID, "%s: bad dtype", what);
   if (int rc = check_count(what, active)) return rc;

@@ -198,6 +198,24 @@ def test_oversized_tensor_is_rejected():
     assert b"too large" in lib.sihc_last_error()
 
 
+def test_token_counts_stop_short_of_int32():
+    # chunk ends (chunks x tokens per chunk < tokens + chunks) and a thread's next token
+    # are int32 in the kernels: token and row counts must stay below 2^31 - 2^16
+    lib = _lib.lib()
+    limit = (1 << 31) - (1 << 16)
+    ups = _lib.ptr_array([FAKE])
+    assert limit % 256 == 0  # limit // 256 batches of a 16 x 16 grid: exactly the limit
+    assert lib.sihc_read(FAKE, FAKE, ups, 1, limit // 256, 16, 2, 64, None, 1, None) == 1
+    assert b"too large" in lib.sihc_last_error()
+    assert lib.sihc_triangular(FAKE, ups, FAKE, FAKE, 1, limit, 64, 1, 0, None) == 1
+    assert b"bad sizes" in lib.sihc_last_error()
+    assert lib.sihc_triangular_gamma_grad(FAKE, ups, FAKE, 1, limit, 64, 1, 0, FAKE, 1 << 30, None) == 1
+    assert b"bad sizes" in lib.sihc_last_error()
+    assert lib.sihc_triangular_backward(FAKE, ups, FAKE, ups, FAKE, 1, limit, 64, 1, 0, 0, FAKE, 1 << 30,
+                                        None) == 1
+    assert b"bad sizes" in lib.sihc_last_error()
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libsihc_hip.so")
