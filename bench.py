@@ -71,7 +71,7 @@ def parse_args():
     p.add_argument("--tri-backward", choices=("visible", "fused"), default=None,
                    help="--mode model --compile: how the triangular op's traced backward returns the update "
                         "gradients (sihc_hip.sublayer_kernels.COMPILED_TRIANGULAR_BACKWARD)")
-    p.add_argument("--mode", choices=("step", "calibrate", "kernels", "e2e", "model", "stage", "ceiling"),
+    p.add_argument("--mode", choices=("step", "calibrate", "kernels", "e2e", "model", "stage", "ceiling", "valu"),
                    default="step",
                    help="step: the benchmark (default); calibrate: a 1 GiB copy-kernel launch plus single "
                         "event forward/backward launches at the same shape, for HBM counter runs; kernels: "
@@ -371,6 +371,45 @@ def stream_ceiling() -> dict:
         del srcs_t, dsts_t
         torch.cuda.empty_cache()
     return out
+
+
+def valu_rate() -> None:
+    """Sustained vector-ALU rates without packed fp32 (sihc_fma_rate): 4, 8 or 16 independent
+    chains per thread, 4 steps per iteration, 20,000 iterations, on 8 to 32 blocks of 256
+    threads per CU, in three instruction forms: fp32 fma with register operands (v_fma_f32,
+    the form of the kernels' products), with literal constants (v_fmamk_f32), and the bf16
+    pair dot (v_dot2c_f32_bf16, 2 lane-FMAs each). One warm-up launch, then the median of 5
+    launches timed with HIP events. Prints one JSON line per case."""
+    import torch
+
+    from sihc_hip import _lib
+
+    L = _lib.lib()
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    iters = 20000
+    forms = {0: "v_fma_f32 (register operands)", 1: "v_fmamk_f32 (literal constants)", 2: "v_dot2c_f32_bf16"}
+    cases = [(0, 4, 8), (0, 4, 32), (0, 8, 32), (0, 16, 32), (1, 8, 32), (1, 16, 32), (2, 8, 32), (2, 16, 32)]
+    for form, chains, per_cu in cases:
+        blocks = cus * per_cu
+        out = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+        run = lambda: _lib.check(L.sihc_fma_rate(ctypes.c_void_p(out.data_ptr()), chains, form, blocks, iters, st))  # noqa
+        run()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(5):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            run()
+            b.record()
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b) * 1e-3)
+        sec = statistics.median(ts)
+        fmas = blocks * 256 * iters * 4 * chains * (2 if form == 2 else 1)
+        print(json.dumps({"form": forms[form], "chains": chains, "blocks_per_cu": per_cu, "cus": cus,
+                          "ms": round(sec * 1e3, 3), "lane_fma_per_s": fmas / sec,
+                          "lane_fma_per_cu_clock_2p4ghz": round(fmas / sec / cus / 2.4e9, 1),
+                          "finite": bool(torch.isfinite(out).all())}), flush=True)
 
 
 def extra_configs(seed: int) -> dict:
@@ -1120,6 +1159,9 @@ def main():
         return
     if args.mode == "ceiling":
         print(json.dumps(stream_ceiling()), flush=True)
+        return
+    if args.mode == "valu":
+        valu_rate()
         return
     print(f"[bench] building step: batch={args.batch} C={args.channels} events={args.events}", file=sys.stderr,
           flush=True)

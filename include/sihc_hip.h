@@ -267,6 +267,16 @@ int sihc_stream(const void *const *src, int nsrc, void *const *dst, int ndst, si
 int sihc_stream_mix(const void *const *src, int nsrc, int ncar_src, void *const *dst, int ndst,
                     int ncar_dst, int slots, size_t bytes, void *sink, void *stream);
 
+/* Vector-ALU calibration: `blocks` blocks of 256 threads, each running `chains` (4, 8 or 16)
+ * independent accumulation chains for `iters` iterations of 4 steps, then storing one float
+ * per thread to `out` (blocks * 256 floats). form 0: fp32 fma with register operands
+ * (v_fma_f32: chain k of thread t starts at t * 1e-3 + k, a = fma(a, 1.0000001, 1e-7));
+ * form 1: the same with literal constants (v_fmamk_f32); form 2: v_dot2c_f32_bf16, each step
+ * adding (0.5, 0.25) . (0.5, 0.5) = 0.375. lane-FMAs = blocks * 256 * iters * 4 * chains
+ * (x 2 for form 2). No reference counterpart: the arithmetic ceiling the kernels are read
+ * against (bench.py --mode valu). */
+int sihc_fma_rate(void *out, int chains, int form, int blocks, int iters, void *stream);
+
 /* Plain device copy of `bytes` bytes (16-byte vectors). No reference counterpart: it is
  * the calibration kernel for HBM counters and the practical bandwidth ceiling. */
 int sihc_copy(const void *src, void *dst, size_t bytes, void *stream);

@@ -2933,6 +2933,33 @@ __global__ void __launch_bounds__(256) k_stream_mix(PtrPack src, int nsrc, int n
   }
 }
 
+// Vector-ALU calibration: CH independent accumulation chains per thread, 4 steps of each
+// per iteration, one sum per thread stored so no chain can be dropped. FORM 0: fp32 fma
+// with register operands (v_fma_f32, the form the kernels' products take); FORM 1: the
+// multiplier and addend as literal constants (v_fmamk_f32); FORM 2: v_dot2c_f32_bf16 of
+// two bf16 pairs (2 lane-FMAs a step). No packed fp32: the library's flags keep it out.
+template <int CH, int FORM>
+__global__ void __launch_bounds__(256) k_fma_chains(float* __restrict__ out, int iters, float mul, float add,
+                                                    uint32_t pa, uint32_t pb) {
+  float a[CH];
+#pragma unroll
+  for (int k = 0; k < CH; ++k) a[k] = float(threadIdx.x) * 1e-3f + float(k);
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int k = 0; k < CH; ++k) {
+        if constexpr (FORM == 0) a[k] = fmaf(a[k], mul, add);
+        else if constexpr (FORM == 1) a[k] = fmaf(a[k], 1.0000001f, 1e-7f);
+        else a[k] = dot2(pa, pb, a[k]);
+      }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < CH; ++k) s += a[k];
+  out[int64_t(blockIdx.x) * 256 + threadIdx.x] = s;
+}
+
 __global__ void k_copy1(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int64_t n) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) dst[i] = src[i];
@@ -4377,6 +4404,31 @@ int sihc_stream(const void* const* src, int nsrc, void* const* dst, int ndst, si
   if (nsrc == 2 && ndst == 2) return go(k_stream<2, 2, 0, 0>);
   if (nsrc == 4 && ndst == 2) return go(k_stream<4, 2, 0, 0>);
   return go(k_stream<0, 1, 0, 0>);
+}
+
+int sihc_fma_rate(void* out, int chains, int form, int blocks, int iters, void* stream) {
+  const char* what = "sihc_fma_rate";
+  if (chains != 4 && chains != 8 && chains != 16) return fail(SIHC_ERR_INVALID, "%s: chains must be 4, 8 or 16", what);
+  if (form < 0 || form > 2) return fail(SIHC_ERR_INVALID, "%s: form must be 0, 1 or 2", what);
+  if (blocks < 1 || iters < 1) return fail(SIHC_ERR_INVALID, "%s: blocks and iters must be positive", what);
+  if (!out || !aligned(out, 4)) return fail(SIHC_ERR_INVALID, "%s: null or misaligned output", what);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* o = static_cast<float*>(out);
+  // bf16 pairs (0.5, 0.25) . (0.5, 0.5): each dot2 step adds exactly 0.375
+  const uint32_t pa = 0x3e803f00u, pb = 0x3f003f00u;
+  auto go = [&](auto ch) {
+    constexpr int CH = decltype(ch)::value;
+    if (form == 0)
+      hipLaunchKernelGGL((k_fma_chains<CH, 0>), dim3(blocks), dim3(256), 0, st, o, iters, 1.0000001f, 1e-7f, pa, pb);
+    else if (form == 1)
+      hipLaunchKernelGGL((k_fma_chains<CH, 1>), dim3(blocks), dim3(256), 0, st, o, iters, 1.0000001f, 1e-7f, pa, pb);
+    else
+      hipLaunchKernelGGL((k_fma_chains<CH, 2>), dim3(blocks), dim3(256), 0, st, o, iters, 1.0000001f, 1e-7f, pa, pb);
+  };
+  if (chains == 4) go(IC<4>{});
+  else if (chains == 8) go(IC<8>{});
+  else go(IC<16>{});
+  return check_launch(what);
 }
 
 int sihc_stream_mix(const void* const* src, int nsrc, int ncar_src, void* const* dst, int ndst, int ncar_dst,

@@ -55,6 +55,7 @@ PROTOTYPES: dict[str, tuple] = {
     "sihc_stream": (_i32, [_vpp, _i32, _vpp, _i32, _sz, _i32, _vp]),
     "sihc_stream_mix": (_i32, [_vpp, _i32, _i32, _vpp, _i32, _i32, _i32, _sz, _vp, _vp]),
     "sihc_copy": (_i32, [_vp, _vp, _sz, _vp]),
+    "sihc_fma_rate": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
 }
 
 _lock = threading.Lock()

@@ -198,6 +198,18 @@ def test_oversized_tensor_is_rejected():
     assert b"too large" in lib.sihc_last_error()
 
 
+def test_fma_rate_arguments_are_validated():
+    lib = _lib.lib()
+    assert lib.sihc_fma_rate(FAKE, 5, 0, 1, 1, None) == 1
+    assert b"chains must be 4, 8 or 16" in lib.sihc_last_error()
+    assert lib.sihc_fma_rate(FAKE, 4, 3, 1, 1, None) == 1
+    assert b"form must be 0, 1 or 2" in lib.sihc_last_error()
+    assert lib.sihc_fma_rate(FAKE, 4, 0, 0, 1, None) == 1
+    assert b"must be positive" in lib.sihc_last_error()
+    assert lib.sihc_fma_rate(None, 4, 0, 1, 1, None) == 1
+    assert b"null or misaligned" in lib.sihc_last_error()
+
+
 def test_token_counts_stop_short_of_int32():
     # chunk ends (chunks x tokens per chunk < tokens + chunks) and a thread's next token
     # are int32 in the kernels: token and row counts must stay below 2^31 - 2^16

@@ -215,3 +215,35 @@ def test_stream_mix_kernel(ns, ncs, nd, ncd, slots):
         assert torch.equal(sink.view(units, 4, 4), red), "sink"
     else:
         assert not sink.any(), "the sink is written only by read-only mixes"
+
+
+@pytest.mark.parametrize("form", [0, 1, 2], ids=["fma-reg", "fma-literal", "dot2"])
+@pytest.mark.parametrize("chains", [4, 8, 16])
+def test_fma_rate_kernel(chains, form):
+    # sihc_fma_rate (the vector-ALU calibration bench.py --mode valu times): thread t of any
+    # block starts chain k at t * 1e-3 + k, applies a = fma(a, 1.0000001, 1e-7) (forms 0, 1)
+    # or a += (0.5, 0.25) . (0.5, 0.5) = 0.375 (form 2, a bf16 pair dot) 4 x iters times, and
+    # stores the sum of its chains. Checked against a float64 replay rounded to float32 after
+    # every step (the kernel's single rounding may differ in the last bit).
+    import ctypes
+
+    import numpy as np
+
+    from sihc_hip import _lib
+
+    announce(f"fma rate kernel chains={chains} form={form}")
+    blocks, iters = 3, 5
+    out = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+    _lib.check(_lib.lib().sihc_fma_rate(ctypes.c_void_p(out.data_ptr()), chains, form, blocks, iters,
+                                        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    torch.cuda.synchronize()
+    t = np.arange(256, dtype=np.float64)
+    a = np.stack([np.float32(t * 1e-3 + k) for k in range(chains)]).astype(np.float64)
+    for _ in range(4 * iters):
+        if form == 2:
+            a = (a + 0.375).astype(np.float32).astype(np.float64)
+        else:
+            a = (a * np.float64(np.float32(1.0000001)) + np.float64(np.float32(1e-7))).astype(np.float32).astype(np.float64)
+    exp = torch.from_numpy(a.sum(axis=0).astype(np.float32)).repeat(blocks)
+    got = out.cpu()
+    assert torch.allclose(got, exp, rtol=1e-6, atol=0), (got - exp).abs().max()
