@@ -376,9 +376,9 @@ def stream_ceiling() -> dict:
 def valu_rate() -> None:
     """Sustained vector-ALU rates without packed fp32 (sihc_fma_rate): 4, 8 or 16 independent
     chains per thread, 4 steps per iteration, 20,000 iterations, on 8 to 32 blocks of 256
-    threads per CU, in three instruction forms: fp32 fma with register operands (v_fma_f32,
-    the form of the kernels' products), with literal constants (v_fmamk_f32), and the bf16
-    pair dot (v_dot2c_f32_bf16, 2 lane-FMAs each). One warm-up launch, then the median of 5
+    threads per CU, in four instruction forms: fp32 fma with register operands (v_fma_f32),
+    with literal constants (v_fmamk_f32), the bf16 pair dot (v_dot2c_f32_bf16, 2 lane-FMAs
+    each) and the accumulating fma (v_fmac_f32, the form of the kernels' sums). One warm-up launch, then the median of 5
     launches timed with HIP events. Prints one JSON line per case."""
     import torch
 
@@ -388,8 +388,10 @@ def valu_rate() -> None:
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     iters = 20000
-    forms = {0: "v_fma_f32 (register operands)", 1: "v_fmamk_f32 (literal constants)", 2: "v_dot2c_f32_bf16"}
-    cases = [(0, 4, 8), (0, 4, 32), (0, 8, 32), (0, 16, 32), (1, 8, 32), (1, 16, 32), (2, 8, 32), (2, 16, 32)]
+    forms = {0: "v_fma_f32 (register operands)", 1: "v_fmamk_f32 (literal constants)", 2: "v_dot2c_f32_bf16",
+             3: "v_fmac_f32 (accumulating)"}
+    cases = [(0, 4, 8), (0, 4, 32), (0, 8, 32), (0, 16, 32), (1, 8, 32), (1, 16, 32), (2, 8, 32), (2, 16, 32),
+             (3, 8, 32), (3, 16, 32)]
     for form, chains, per_cu in cases:
         blocks = cus * per_cu
         out = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")

@@ -272,7 +272,8 @@ int sihc_stream_mix(const void *const *src, int nsrc, int ncar_src, void *const 
  * per thread to `out` (blocks * 256 floats). form 0: fp32 fma with register operands
  * (v_fma_f32: chain k of thread t starts at t * 1e-3 + k, a = fma(a, 1.0000001, 1e-7));
  * form 1: the same with literal constants (v_fmamk_f32); form 2: v_dot2c_f32_bf16, each step
- * adding (0.5, 0.25) . (0.5, 0.5) = 0.375. lane-FMAs = blocks * 256 * iters * 4 * chains
+ * adding (0.5, 0.25) . (0.5, 0.5) = 0.375; form 3: a = fma(1.0000001, 1e-7, a), the chain as
+ * the addend (v_fmac_f32). lane-FMAs = blocks * 256 * iters * 4 * chains
  * (x 2 for form 2). No reference counterpart: the arithmetic ceiling the kernels are read
  * against (bench.py --mode valu). */
 int sihc_fma_rate(void *out, int chains, int form, int blocks, int iters, void *stream);

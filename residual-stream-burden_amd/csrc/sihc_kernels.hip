@@ -2937,7 +2937,9 @@ __global__ void __launch_bounds__(256) k_stream_mix(PtrPack src, int nsrc, int n
 // per iteration, one sum per thread stored so no chain can be dropped. FORM 0: fp32 fma
 // with register operands (v_fma_f32, the form the kernels' products take); FORM 1: the
 // multiplier and addend as literal constants (v_fmamk_f32); FORM 2: v_dot2c_f32_bf16 of
-// two bf16 pairs (2 lane-FMAs a step). No packed fp32: the library's flags keep it out.
+// two bf16 pairs (2 lane-FMAs a step); FORM 3: the chain value as the addend, a = fma(mul,
+// add, a) (v_fmac_f32, the form of the kernels' accumulations). No packed fp32: the
+// library's flags keep it out.
 template <int CH, int FORM>
 __global__ void __launch_bounds__(256) k_fma_chains(float* __restrict__ out, int iters, float mul, float add,
                                                     uint32_t pa, uint32_t pb) {
@@ -2951,7 +2953,8 @@ __global__ void __launch_bounds__(256) k_fma_chains(float* __restrict__ out, int
       for (int k = 0; k < CH; ++k) {
         if constexpr (FORM == 0) a[k] = fmaf(a[k], mul, add);
         else if constexpr (FORM == 1) a[k] = fmaf(a[k], 1.0000001f, 1e-7f);
-        else a[k] = dot2(pa, pb, a[k]);
+        else if constexpr (FORM == 2) a[k] = dot2(pa, pb, a[k]);
+        else a[k] = fmaf(mul, add, a[k]);
       }
   }
   float s = 0.f;
@@ -4409,7 +4412,7 @@ int sihc_stream(const void* const* src, int nsrc, void* const* dst, int ndst, si
 int sihc_fma_rate(void* out, int chains, int form, int blocks, int iters, void* stream) {
   const char* what = "sihc_fma_rate";
   if (chains != 4 && chains != 8 && chains != 16) return fail(SIHC_ERR_INVALID, "%s: chains must be 4, 8 or 16", what);
-  if (form < 0 || form > 2) return fail(SIHC_ERR_INVALID, "%s: form must be 0, 1 or 2", what);
+  if (form < 0 || form > 3) return fail(SIHC_ERR_INVALID, "%s: form must be 0..3", what);
   if (blocks < 1 || iters < 1) return fail(SIHC_ERR_INVALID, "%s: blocks and iters must be positive", what);
   if (!out || !aligned(out, 4)) return fail(SIHC_ERR_INVALID, "%s: null or misaligned output", what);
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -4422,8 +4425,10 @@ int sihc_fma_rate(void* out, int chains, int form, int blocks, int iters, void* 
       hipLaunchKernelGGL((k_fma_chains<CH, 0>), dim3(blocks), dim3(256), 0, st, o, iters, 1.0000001f, 1e-7f, pa, pb);
     else if (form == 1)
       hipLaunchKernelGGL((k_fma_chains<CH, 1>), dim3(blocks), dim3(256), 0, st, o, iters, 1.0000001f, 1e-7f, pa, pb);
-    else
+    else if (form == 2)
       hipLaunchKernelGGL((k_fma_chains<CH, 2>), dim3(blocks), dim3(256), 0, st, o, iters, 1.0000001f, 1e-7f, pa, pb);
+    else
+      hipLaunchKernelGGL((k_fma_chains<CH, 3>), dim3(blocks), dim3(256), 0, st, o, iters, 1.0000001f, 1e-7f, pa, pb);
   };
   if (chains == 4) go(IC<4>{});
   else if (chains == 8) go(IC<8>{});

@@ -202,8 +202,8 @@ def test_fma_rate_arguments_are_validated():
     lib = _lib.lib()
     assert lib.sihc_fma_rate(FAKE, 5, 0, 1, 1, None) == 1
     assert b"chains must be 4, 8 or 16" in lib.sihc_last_error()
-    assert lib.sihc_fma_rate(FAKE, 4, 3, 1, 1, None) == 1
-    assert b"form must be 0, 1 or 2" in lib.sihc_last_error()
+    assert lib.sihc_fma_rate(FAKE, 4, 4, 1, 1, None) == 1
+    assert b"form must be 0..3" in lib.sihc_last_error()
     assert lib.sihc_fma_rate(FAKE, 4, 0, 0, 1, None) == 1
     assert b"must be positive" in lib.sihc_last_error()
     assert lib.sihc_fma_rate(None, 4, 0, 1, 1, None) == 1

@@ -217,12 +217,13 @@ def test_stream_mix_kernel(ns, ncs, nd, ncd, slots):
         assert not sink.any(), "the sink is written only by read-only mixes"
 
 
-@pytest.mark.parametrize("form", [0, 1, 2], ids=["fma-reg", "fma-literal", "dot2"])
+@pytest.mark.parametrize("form", [0, 1, 2, 3], ids=["fma-reg", "fma-literal", "dot2", "fmac"])
 @pytest.mark.parametrize("chains", [4, 8, 16])
 def test_fma_rate_kernel(chains, form):
     # sihc_fma_rate (the vector-ALU calibration bench.py --mode valu times): thread t of any
     # block starts chain k at t * 1e-3 + k, applies a = fma(a, 1.0000001, 1e-7) (forms 0, 1)
-    # or a += (0.5, 0.25) . (0.5, 0.5) = 0.375 (form 2, a bf16 pair dot) 4 x iters times, and
+    # or a += (0.5, 0.25) . (0.5, 0.5) = 0.375 (form 2, a bf16 pair dot) or a = fma(1.0000001,
+    # 1e-7, a) (form 3, the accumulating form) 4 x iters times, and
     # stores the sum of its chains. Checked against a float64 replay rounded to float32 after
     # every step (the kernel's single rounding may differ in the last bit).
     import ctypes
@@ -242,6 +243,8 @@ def test_fma_rate_kernel(chains, form):
     for _ in range(4 * iters):
         if form == 2:
             a = (a + 0.375).astype(np.float32).astype(np.float64)
+        elif form == 3:
+            a = (a + np.float64(np.float32(1.0000001)) * np.float64(np.float32(1e-7))).astype(np.float32).astype(np.float64)
         else:
             a = (a * np.float64(np.float32(1.0000001)) + np.float64(np.float32(1e-7))).astype(np.float32).astype(np.float64)
     exp = torch.from_numpy(a.sum(axis=0).astype(np.float32)).repeat(blocks)
