@@ -42,7 +42,7 @@ extern "C" {
 /* Tokens (batch*grid*grid) or workspace rows per call: fewer than 2^31 - 2^16, so a chunk's
  * end (chunks x tokens-per-chunk < tokens + chunks) and a thread's next token stay in int32. */
 #define SIHC_MAX_TOKENS (((int64_t)1 << 31) - ((int64_t)1 << 16))
-#define SIHC_ABI_VERSION 4
+#define SIHC_ABI_VERSION 5
 /* Bytes of the per-GPU scratch array of sihc_event_backward_noalloc (64 MiB). */
 #define SIHC_SCRATCH_BYTES (64u << 20)
 

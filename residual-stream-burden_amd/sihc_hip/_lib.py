@@ -10,7 +10,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libsihc_hip.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 MAX_EVENTS = 32
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
